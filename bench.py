@@ -1,0 +1,212 @@
+#!/usr/bin/env python
+"""Benchmark of the draft-objective hot path on one MI355X.
+
+Metric: draft slots/sec, forward + backward (CE + KL + accept_len forward, dl,
+and dhidden when the LM head is fused), with the dominant kernel's roofline
+fraction.  A "step" is one pass of the hot path over one batch of synthetic
+input that is already resident in HBM.
+
+    python bench.py [--steps K] [--warmup W] [--config c1|c2|c3|c4]
+
+Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a
+message (the path is data-parallel over slots; the library has no collectives).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA, TFLOP/s
+
+METRIC = "draft slots/sec fwd+bwd CE+KL+accept @V=248k,d=5120; %MFMA & %HBM roof"
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", default="c1", choices=["c1", "c2", "c3", "c4"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU-baseline sample (0: default)")
+    return p.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+# --------------------------------------------------------------------------- C1
+
+
+def workload_c1(device, args):
+    import torch
+
+    from nanospec_amd import objective, synthetic
+    from nanospec_amd.config import Objective
+
+    z, u, slots = synthetic.c1(device)
+    n, v = z.shape
+    o = Objective(block_size=8, gamma=4.0)
+
+    def step():
+        metrics, saved = objective.ce_kl_loss(z, u, slots, o)
+        dl = objective.ce_kl_backward(saved)
+        return metrics, dl
+
+    # algorithmic bytes per slot: read z (bf16) + read u (bf16) + write dl (bf16)
+    per_slot = 6 * v
+    kernel_bytes = {
+        "stream_stats": 4 * v * n,   # read z, u
+        "stream_emit": 6 * v * n,    # read z, u, write dl
+    }
+
+    def cpu_baseline(rows):
+        import numpy as np
+
+        from oracle import objective_ref as ref
+
+        rows = rows or 256
+        zs = z[:rows].float().cpu().numpy()
+        us = u[:rows].float().cpu().numpy()
+        w = slots.weights.reshape(-1)[:rows].cpu().numpy()
+        y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
+        vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
+        t0 = time.perf_counter()
+        ref.ce_kl_loss(zs, us, w.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
+                       dtype=np.float32, chunk_rows=32)
+        ref.ce_kl_backward(zs, us, w, y, o.ce, o.kl, 1, dtype=np.float32)
+        dt = time.perf_counter() - t0
+        return dict(value=rows / dt, unit="slots/s", cores=1, kind="port",
+                    sample=f"numpy fp32 oracle (oracle/objective_ref.py), single thread, {rows} of the "
+                           f"{n} C1 rows ({rows // 8} whole blocks), V={v}: ce_kl_loss + ce_kl_backward; "
+                           f"{dt:.2f} s")
+
+    config = {"workload": "C1 logits-only: CE+KL+accept fwd + dlogits bwd over given bf16 [N,V] logits",
+              "N": n, "V": v, "K": 8, "gamma": 4.0, "masked_rows": int((~slots.valid).sum()),
+              "global_batch": n, "parallelism": "single GPU"}
+    return dict(step=step, n=n, per_slot_bytes=per_slot, per_slot_flops=None, kernel_bytes=kernel_bytes,
+                kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16")
+
+
+WORKLOADS = {"c1": workload_c1}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the "
+              "objective path is data-parallel over slots with no collectives in this library; see "
+              "DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+    if args.config not in WORKLOADS:
+        print(f"config {args.config} is not available in this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from nanospec_amd import _lib
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    _lib.load()
+    wl = WORKLOADS[args.config](device, args)
+    step = wl["step"]
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed window: exactly K steps between two device synchronisations
+    start_ev, stop_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start_ev.record()
+    for _ in range(args.steps):
+        step()
+    stop_ev.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start_ev.elapsed_time(stop_ev)
+    ms_per_step = gpu_ms / args.steps
+    n = wl["n"]
+    value = n * args.steps / (gpu_ms / 1e3)
+
+    # kernel durations: HIP events recorded by the library on each launch's stream
+    with _lib.KernelTimer() as kt:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    kernels = {name: {"launches": c, "mean_ms": tot / max(c, 1)} for name, (c, tot) in kt.times.items()}
+    dominant = max(kt.times, key=lambda k: kt.times[k][1])
+    dom_ms = kernels[dominant]["mean_ms"]
+    if dominant in wl["kernel_flops"]:
+        achieved = wl["kernel_flops"][dominant] / (dom_ms / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / BF16_PEAK_TFLOPS}
+    else:
+        achieved = wl["kernel_bytes"].get(dominant, 0) / (dom_ms / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+    roof["kernel"] = dominant
+    roof["kernel_mean_ms"] = dom_ms
+    roof["traffic"] = None
+    for name, info in kernels.items():
+        if name in wl["kernel_bytes"]:
+            info["algorithmic_GBs"] = wl["kernel_bytes"][name] / (info["mean_ms"] / 1e3) / 1e9
+        if name in wl["kernel_flops"]:
+            info["algorithmic_TFLOPs"] = wl["kernel_flops"][name] / (info["mean_ms"] / 1e3) / 1e12
+    step_roof = {}
+    if wl["per_slot_bytes"]:
+        step_roof["algorithmic_GBs"] = wl["per_slot_bytes"] * n / (ms_per_step / 1e3) / 1e9
+        step_roof["hbm_frac"] = step_roof["algorithmic_GBs"] / HBM_PEAK_GBS
+    if wl["per_slot_flops"]:
+        step_roof["algorithmic_TFLOPs"] = wl["per_slot_flops"] * n / (ms_per_step / 1e3) / 1e12
+        step_roof["mfma_frac"] = step_roof["algorithmic_TFLOPs"] / BF16_PEAK_TFLOPS
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = wl["cpu_baseline"](args.cpu_rows)
+
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "slots/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl["dtype"],
+        "data": "synthetic (seeded; distributions of BASELINE.json configs)",
+        "config": wl["config"],
+        "roofline": roof,
+        "step_roofline": step_roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "wall_s": wall,
+        "host": {"cpu_model": cpu_model(), "cpu_count": os.cpu_count()},
+        "device": torch.cuda.get_device_name(device),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

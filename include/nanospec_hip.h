@@ -1,0 +1,102 @@
+/* nanospec_hip.h -- C ABI of the MI355X (gfx950) draft-objective library.
+ *
+ * Drop-in for the arithmetic of nanospec's draft head + objective path
+ * (reference paths relative to the jamesdborin/nanospec checkout):
+ *   nanospec/objective.py:49-67   ce_kl_loss         -> ns_ce_kl_logits_fwd
+ *   nanospec/objective.py:70-80   ce_kl_backward     -> ns_ce_kl_logits_bwd
+ *   nanospec/objective.py:39-46   acceptance_length_counts (inside both fwd entries)
+ *   nanospec/ops.py:34-35 via train.py:272-279, 291   linear + ce_kl_loss fused
+ *                                                     -> ns_lmhead_ce_kl_fwd
+ *   nanospec/train.py:302         dh = dl @ lm_head.w -> ns_lmhead_bwd
+ *
+ * Conventions
+ *   - All tensor arguments are device pointers; rows are `ld` elements apart,
+ *     elements within a row are contiguous.
+ *   - Every call is asynchronous on `stream` (the caller's current HIP stream);
+ *     nothing synchronises the device and nothing is allocated: scratch
+ *     memory is passed in as `workspace` (size from the *_workspace_bytes query).
+ *   - Status: 0 ok; negative = invalid argument (shape, dtype, alignment,
+ *     workspace size); positive = hipError_t from a launch.  ns_last_error()
+ *     returns a thread-local description of the last failure.
+ *   - dtype codes: NS_BF16 (raw bfloat16) or NS_F32.
+ *   - Row metadata: labels int64 [N], weights fp32 [N] (valid * exp(-slot/gamma)),
+ *     valid uint8 [N] (torch.bool); rows come in blocks of K consecutive slots.
+ *   - Outputs: metrics fp32 [6] in LossMetrics order (ce, kl, numerator,
+ *     denominator, accept_len_sum, accept_len_total; objective.py:11-18) and
+ *     row_stats fp32 [N][8] = (lse_z, lse_u, ce, kl, accept_rate, z_label, 0, 0).
+ */
+#ifndef NANOSPEC_HIP_H
+#define NANOSPEC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NS_ABI_VERSION 1
+
+#define NS_BF16 0
+#define NS_F32 1
+
+#define NS_OK 0
+#define NS_EINVAL (-1)     /* bad shape or scalar argument */
+#define NS_EDTYPE (-2)     /* unsupported dtype code */
+#define NS_EALIGN (-3)     /* pointer / leading-dimension alignment */
+#define NS_EWORKSPACE (-4) /* workspace missing or too small */
+#define NS_ENULL (-5)      /* required pointer is NULL */
+
+#define NS_WS_LOGITS 0   /* ns_ce_kl_logits_fwd */
+#define NS_WS_LMHEAD 1   /* ns_lmhead_ce_kl_fwd */
+#define NS_WS_LMHEAD_BWD 2 /* ns_lmhead_bwd */
+#define NS_WS_FP8 3      /* ns_fp8_teacher_logits */
+
+typedef struct ihipStream_t* ns_stream_t; /* == hipStream_t */
+
+/* Library ABI version (NS_ABI_VERSION); the loader refuses a mismatch. */
+int ns_abi_version(void);
+
+/* Thread-local text of the last non-zero status. */
+const char* ns_last_error(void);
+
+/* Scratch bytes an entry point of `kind` needs (NS_WS_*); d is ignored by
+ * NS_WS_LOGITS, v by NS_WS_FP8. */
+size_t ns_workspace_bytes(int kind, int64_t n, int64_t v, int64_t d);
+
+/* Forward objective over given logits (objective.py:49-67) plus, when dl is not
+ * NULL, the derivative of objective.py:70-80 with scale inv_acc = 1/accumulation_steps.
+ * z: draft logits [N, V] (z_dtype); u: teacher logits [N, V] (u_dtype);
+ * dl: [N, V] in z_dtype, or NULL.  n % k == 0. */
+int ns_ce_kl_logits_fwd(const void* z, int z_dtype, int64_t ldz, const void* u, int u_dtype, int64_t ldu,
+                        const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n,
+                        int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd,
+                        float* row_stats, float* metrics, void* workspace, size_t workspace_bytes,
+                        ns_stream_t stream);
+
+/* dl alone (objective.py:70-80) from row_stats of a previous forward. */
+int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, int u_dtype, int64_t ldu,
+                        const int64_t* labels, const float* weights, int64_t n, int64_t v, float c_ce,
+                        float c_kl, float inv_acc, const float* row_stats, void* dl, int64_t ldd,
+                        ns_stream_t stream);
+
+/* ---- timing instrumentation (opt-in) -------------------------------------
+ * Between ns_profile_begin() and ns_profile_end(), every kernel the library
+ * launches is bracketed by HIP events recorded on its launch stream.
+ * ns_profile_end() waits for those events and fills up to `capacity` entries
+ * (one per kernel name, in first-launch order); *count receives the number of
+ * distinct kernels.  Not for use while another thread calls the library. */
+typedef struct {
+  char name[48];
+  int launches;
+  double total_ms;
+} ns_kernel_time;
+
+int ns_profile_begin(void);
+int ns_profile_end(ns_kernel_time* out, int capacity, int* count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOSPEC_HIP_H */

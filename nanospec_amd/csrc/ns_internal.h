@@ -1,0 +1,68 @@
+// Internal launch interface shared by the kernel sources and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ns_common.h"
+
+namespace ns {
+
+// Inputs shared by every objective entry point (all device pointers).
+struct SlotArgs {
+  const int64_t* labels;   // [N] target token ids (prepared.target_ids)
+  const float* weights;    // [N] w = valid * exp(-slot/gamma) (prepared.weights)
+  const uint8_t* valid;    // [N] supervision validity (prepared.valid, torch.bool)
+  int64_t n;               // rows (draft slots)
+  int64_t k;               // slots per block (accept_len prefix axis)
+  float c_ce, c_kl;        // objective.ce, objective.kl
+  float inv_acc;           // 1 / accumulation_steps
+};
+
+// ---- logits-level streaming path (stream.hip) -----------------------------
+int stream_splits(int64_t n, int64_t v);
+size_t stream_workspace_bytes(int64_t n, int64_t v);
+hipError_t stream_forward(const void* z, int zdt, int64_t ldz, const void* u, int udt, int64_t ldu,
+                          int64_t v, const SlotArgs& a, void* dl, int64_t ldd, float* row_stats,
+                          float* metrics, void* ws, hipStream_t st);
+hipError_t stream_backward(const void* z, int zdt, int64_t ldz, const void* u, int udt, int64_t ldu,
+                           int64_t v, const SlotArgs& a, const float* row_stats, void* dl, int64_t ldd,
+                           hipStream_t st);
+
+// ---- shared tails (stream.hip) ---------------------------------------------
+// Merge first-pass partials part1[N][S] (+ z_y[N]) into row_stats (lse_z, lse_u, ce, kl, z_y).
+hipError_t launch_merge(const RowPart* part1, const float* zy, int64_t v, int splits, const SlotArgs& a,
+                        float* row_stats, hipStream_t st);
+// Sum accept partials parta[N][S], form block lengths and the six metrics.
+hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, float* row_stats,
+                           float* metrics, hipStream_t st);
+
+// ---- fused LM-head path (lmhead.hip) ---------------------------------------
+size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d);
+hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                          const void* markov, int64_t ldm, const void* teacher, int tdt, int64_t ldt,
+                          int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd,
+                          float* row_stats, float* metrics, void* ws, hipStream_t st);
+size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d);
+hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh,
+                           int64_t lddh, int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st);
+hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
+                         int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d,
+                         hipStream_t st);
+
+// ---- FP8 teacher head (fp8.hip) ---------------------------------------------
+size_t fp8_workspace_bytes(int64_t n, int64_t d);
+hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw,
+                              const float* scale, void* out, int64_t ldo, int64_t n, int64_t v,
+                              int64_t d, void* ws, hipStream_t st);
+
+// ---- slot preparation (prepare.hip) -----------------------------------------
+hipError_t prepare_slots(const int64_t* ids, const float* loss_mask, const int64_t* anchors,
+                         const uint8_t* keep, int64_t b, int64_t s, int64_t nb, int64_t k,
+                         float gamma, int64_t* target_ids, int64_t* previous, float* weights,
+                         uint8_t* valid, int64_t* teacher_indices, hipStream_t st);
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace ns

@@ -1,0 +1,399 @@
+// Logits-level draft objective: CE + KL(target || draft) + accept rate and dl,
+// streamed over given [N, V] draft (z) and teacher (u) logits.
+//
+// Restates nanospec/objective.py:49-80 (ce_kl_loss / ce_kl_backward) and
+// objective.py:39-46 (acceptance_length_counts) without materialising any
+// [N, V] probability tensor:
+//   pass 1  (stats)   per (row, vocab split): online (max, sum-exp) of z and u and
+//                     A = sum exp(u - m_u)(u - z)              -> RowPart partials
+//   merge             per row: LSE_z, LSE_u, CE = LSE_z - z_y,
+//                     KL = A / s_u - LSE_u + LSE_z              -> row_stats
+//   pass 2  (emit)    per (row, vocab split): p, t; sum min(p, t); optionally
+//                     dl = (w/acc)[(c_ce + c_kl) p - c_kl t - c_ce e_y]
+//   finalize          one workgroup: accept rate per row, block prefix
+//                     lengths, the six LossMetrics scalars (fixed order).
+// Every reduction has a fixed order, so results are bitwise reproducible.
+#include "ns_internal.h"
+#include "ns_profile.h"
+
+namespace ns {
+
+constexpr int kStreamThreads = 256;
+constexpr int64_t kElemsPerBlock = 16384;   // target vocab elements per workgroup
+constexpr int kMaxSplits = 64;
+
+int stream_splits(int64_t n, int64_t v) {
+  (void)n;
+  int64_t s = (v + kElemsPerBlock - 1) / kElemsPerBlock;
+  if (s < 1) s = 1;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return (int)s;
+}
+
+static inline int64_t split_chunk(int64_t v, int splits) {
+  const int64_t c = (v + splits - 1) / splits;
+  return (c + 7) / 8 * 8;
+}
+
+struct StreamWs {
+  RowPart* part1;
+  float* parta;
+  float* zy;
+};
+
+static size_t stream_ws_layout(int64_t n, int64_t v, void* base, StreamWs* out) {
+  const int S = stream_splits(n, v);
+  const size_t b1 = align_up((size_t)n * S * sizeof(RowPart), 256);
+  const size_t b2 = align_up((size_t)n * S * sizeof(float), 256);
+  const size_t b3 = align_up((size_t)n * sizeof(float), 256);
+  if (out) {
+    char* p = static_cast<char*>(base);
+    out->part1 = reinterpret_cast<RowPart*>(p);
+    out->parta = reinterpret_cast<float*>(p + b1);
+    out->zy = reinterpret_cast<float*>(p + b1 + b2);
+  }
+  return b1 + b2 + b3;
+}
+
+size_t stream_workspace_bytes(int64_t n, int64_t v) { return stream_ws_layout(n, v, nullptr, nullptr); }
+
+// Block-wide merge of pair states; thread 0 returns the result.
+__device__ __forceinline__ PairState block_reduce_pair(PairState st) {
+  __shared__ PairState sh[kStreamThreads / 64];
+  st = wave_reduce(st);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) sh[wave] = st;
+  __syncthreads();
+  PairState r = sh[0];
+#pragma unroll
+  for (int w = 1; w < kStreamThreads / 64; ++w) r = pair_merge(r, sh[w]);
+  return r;
+}
+
+__device__ __forceinline__ float block_sum(float x) {
+  __shared__ float sh[kStreamThreads / 64];
+  x = wave_sum(x);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) sh[wave] = x;
+  __syncthreads();
+  float r = sh[0];
+#pragma unroll
+  for (int w = 1; w < kStreamThreads / 64; ++w) r += sh[w];
+  return r;
+}
+
+// ---------------------------------------------------------------- pass 1
+
+template <typename TZ, typename TU, bool VEC>
+__global__ __launch_bounds__(kStreamThreads) void stream_stats_kernel(
+    const TZ* __restrict__ z, int64_t ldz, const TU* __restrict__ u, int64_t ldu, int64_t v,
+    int64_t chunk, int splits, const int64_t* __restrict__ labels, RowPart* __restrict__ part1,
+    float* __restrict__ zy) {
+  const int s = (int)(blockIdx.x % (unsigned)splits);
+  const int64_t r = blockIdx.x / (unsigned)splits;
+  const int64_t lo = (int64_t)s * chunk;
+  const int64_t hi = lo + chunk < v ? lo + chunk : v;
+  const TZ* zr = z + r * ldz;
+  const TU* ur = u + r * ldu;
+  PairState st = pair_init();
+  int64_t scalar_from = lo;
+  if (VEC && lo < hi) {
+    const int64_t nvec = (hi - lo) >> 3;
+    const TZ* zb = zr + lo;
+    const TU* ub = ur + lo;
+    int64_t j = threadIdx.x;
+    for (; j + kStreamThreads < nvec; j += 2 * kStreamThreads) {
+      float zf[16], uf[16];
+      load8(zb + j * 8, zf);
+      load8(ub + j * 8, uf);
+      load8(zb + (j + kStreamThreads) * 8, zf + 8);
+      load8(ub + (j + kStreamThreads) * 8, uf + 8);
+      pair_update<16>(st, zf, uf);
+    }
+    if (j < nvec) {
+      float zf[8], uf[8];
+      load8(zb + j * 8, zf);
+      load8(ub + j * 8, uf);
+      pair_update<8>(st, zf, uf);
+    }
+    scalar_from = lo + nvec * 8;
+  }
+  for (int64_t i = scalar_from + threadIdx.x; i < hi; i += kStreamThreads) {
+    float zf[1] = {load1(zr + i)}, uf[1] = {load1(ur + i)};
+    pair_update<1>(st, zf, uf);
+  }
+  st = block_reduce_pair(st);
+  if (threadIdx.x == 0) {
+    RowPart p;
+    p.mz = st.mz; p.sz = st.sz; p.mu = st.mu; p.su = st.su; p.A = st.A;
+    p.pad0 = p.pad1 = p.pad2 = 0.f;
+    part1[r * splits + s] = p;
+    const int64_t y = labels[r];
+    if (y >= lo && y < hi) zy[r] = load1(zr + y);
+  }
+}
+
+// ---------------------------------------------------------------- merge
+
+__global__ __launch_bounds__(256) void merge_kernel(const RowPart* __restrict__ part1,
+                                                    const float* __restrict__ zy,
+                                                    const int64_t* __restrict__ labels, int64_t v,
+                                                    int splits, int64_t n, float* __restrict__ row_stats) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const RowPart* p = part1 + r * splits;
+  PairState st = {p[0].mz, p[0].sz, p[0].mu, p[0].su, p[0].A};
+  for (int s = 1; s < splits; ++s) st = pair_merge(st, PairState{p[s].mz, p[s].sz, p[s].mu, p[s].su, p[s].A});
+  const float lz = st.mz + logf(st.sz);
+  const float lu = st.mu + logf(st.su);
+  // A label outside [0, V) has no logit: CE becomes NaN (the loss reports it, never masks it).
+  const int64_t label = labels[r];
+  const float y = (label >= 0 && label < v) ? zy[r] : __builtin_nanf("");
+  float* o = row_stats + r * kRowStatWidth;
+  o[kLseZ] = lz;
+  o[kLseU] = lu;
+  o[kCE] = lz - y;
+  o[kKL] = st.A / st.su - lu + lz;
+  o[kZy] = y;
+}
+
+hipError_t launch_merge(const RowPart* part1, const float* zy, int64_t v, int splits, const SlotArgs& a,
+                        float* row_stats, hipStream_t st) {
+  const int64_t blocks = (a.n + 255) / 256;
+  NS_TIMED("merge_rows", st);
+  if (blocks > 0)
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part1, zy, a.labels, v,
+                       splits, a.n, row_stats);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- pass 2
+
+template <typename TZ, typename TU, typename TD, bool VEC, bool EMIT, bool ACCEPT>
+__global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
+    const TZ* __restrict__ z, int64_t ldz, const TU* __restrict__ u, int64_t ldu, int64_t v,
+    int64_t chunk, int splits, const float* __restrict__ row_stats, const int64_t* __restrict__ labels,
+    const float* __restrict__ weights, float c_ce, float c_kl, float inv_acc, TD* __restrict__ dl,
+    int64_t ldd, float* __restrict__ parta) {
+  const int s = (int)(blockIdx.x % (unsigned)splits);
+  const int64_t r = blockIdx.x / (unsigned)splits;
+  const int64_t lo = (int64_t)s * chunk;
+  const int64_t hi = lo + chunk < v ? lo + chunk : v;
+  const TZ* zr = z + r * ldz;
+  const TU* ur = u + r * ldu;
+  TD* dr = EMIT ? dl + r * ldd : nullptr;
+  const float lzl = row_stats[r * kRowStatWidth + kLseZ] * kLog2e;
+  const float lul = row_stats[r * kRowStatWidth + kLseU] * kLog2e;
+  const float w = weights[r] * inv_acc;
+  const float cp = w * (c_ce + c_kl), ct = w * c_kl, cy = w * c_ce;
+  const int64_t y = labels[r];
+  float acc = 0.f;
+  int64_t scalar_from = lo;
+  if (VEC && lo < hi) {
+    const int64_t nvec = (hi - lo) >> 3;
+    for (int64_t j = threadIdx.x; j < nvec; j += kStreamThreads) {
+      const int64_t i0 = lo + j * 8;
+      float zf[8], uf[8], d[8];
+      load8(zr + i0, zf);
+      load8(ur + i0, uf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = fast_exp2(__builtin_fmaf(zf[e], kLog2e, -lzl));
+        const float t = fast_exp2(__builtin_fmaf(uf[e], kLog2e, -lul));
+        if (ACCEPT) acc += fminf(p, t);
+        if (EMIT) d[e] = __builtin_fmaf(cp, p, -ct * t);
+      }
+      if (EMIT) {
+        if ((uint64_t)(y - i0) < 8ull) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (i0 + e == y) d[e] -= cy;
+        }
+        store8(dr + i0, d);
+      }
+    }
+    scalar_from = lo + nvec * 8;
+  }
+  for (int64_t i = scalar_from + threadIdx.x; i < hi; i += kStreamThreads) {
+    const float p = fast_exp2(__builtin_fmaf(load1(zr + i), kLog2e, -lzl));
+    const float t = fast_exp2(__builtin_fmaf(load1(ur + i), kLog2e, -lul));
+    if (ACCEPT) acc += fminf(p, t);
+    if (EMIT) {
+      float d = __builtin_fmaf(cp, p, -ct * t);
+      if (i == y) d -= cy;
+      store1(dr + i, d);
+    }
+  }
+  if (ACCEPT) {
+    acc = block_sum(acc);
+    if (threadIdx.x == 0) parta[r * splits + s] = acc;
+  }
+}
+
+// ---------------------------------------------------------------- finalize
+
+constexpr int kFinalThreads = 1024;
+
+__global__ __launch_bounds__(kFinalThreads) void finalize_kernel(
+    const float* __restrict__ parta, int splits, int64_t n, int64_t k, const float* __restrict__ weights,
+    const uint8_t* __restrict__ valid, float c_ce, float c_kl, float* __restrict__ row_stats,
+    float* __restrict__ metrics) {
+  // phase 1: accept rate per row (fixed split order)
+  if (parta != nullptr) {
+    for (int64_t r = threadIdx.x; r < n; r += kFinalThreads) {
+      const float* p = parta + r * splits;
+      float a = p[0];
+      for (int s = 1; s < splits; ++s) a += p[s];
+      row_stats[r * kRowStatWidth + kAccept] = a;
+    }
+  }
+  __syncthreads();
+  // phase 2: weighted sums and block prefix lengths (objective.py:42-46, 53-60)
+  double den = 0.0, ce = 0.0, kl = 0.0, asum = 0.0, atot = 0.0;
+  const int64_t nblocks = n / k;
+  for (int64_t b = threadIdx.x; b < nblocks; b += kFinalThreads) {
+    double prod = 1.0, len = 1.0;
+    bool any = false;
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t r = b * k + j;
+      const float* rs = row_stats + r * kRowStatWidth;
+      const bool vr = valid[r] != 0;
+      prod *= vr ? (double)rs[kAccept] : 0.0;
+      len += prod;
+      any = any || vr;
+      const double w = weights[r];
+      den += w;
+      ce += w * (double)rs[kCE];
+      kl += w * (double)rs[kKL];
+    }
+    if (any) {
+      asum += len;
+      atot += 1.0;
+    }
+  }
+  __shared__ double sh[5][kFinalThreads / 64];
+  double vals[5] = {den, ce, kl, asum, atot};
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const double x = wave_sum(vals[i]);
+    if ((threadIdx.x & 63) == 0) sh[i][wave] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t[5];
+    for (int i = 0; i < 5; ++i) {
+      t[i] = sh[i][0];
+      for (int w = 1; w < kFinalThreads / 64; ++w) t[i] += sh[i][w];
+    }
+    const double dc = t[0] > 1e-6 ? t[0] : 1e-6;
+    metrics[kMetCE] = (float)(t[1] / dc);
+    metrics[kMetKL] = (float)(t[2] / dc);
+    metrics[kMetNum] = (float)((double)c_ce * t[1] + (double)c_kl * t[2]);
+    metrics[kMetDen] = (float)t[0];
+    metrics[kMetAccSum] = (float)t[3];
+    metrics[kMetAccTot] = (float)t[4];
+  }
+}
+
+hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, float* row_stats,
+                           float* metrics, hipStream_t st) {
+  NS_TIMED("finalize_metrics", st);
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kFinalThreads), 0, st, parta, splits, a.n, a.k,
+                     a.weights, a.valid, a.c_ce, a.c_kl, row_stats, metrics);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- host dispatch
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename TZ, typename TU>
+static hipError_t stats_dispatch(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v,
+                                 const SlotArgs& a, const StreamWs& w, int S, hipStream_t st) {
+  const TZ* zp = static_cast<const TZ*>(z);
+  const TU* up = static_cast<const TU*>(u);
+  const bool vec = aligned16(z) && aligned16(u) && (ldz * (int64_t)sizeof(TZ)) % 16 == 0 &&
+                   (ldu * (int64_t)sizeof(TU)) % 16 == 0;
+  const int64_t chunk = split_chunk(v, S);
+  dim3 grid((unsigned)(S * a.n));
+  NS_TIMED("stream_stats", st);
+  if (vec)
+    hipLaunchKernelGGL((stream_stats_kernel<TZ, TU, true>), grid, dim3(kStreamThreads), 0, st, zp, ldz, up,
+                       ldu, v, chunk, S, a.labels, w.part1, w.zy);
+  else
+    hipLaunchKernelGGL((stream_stats_kernel<TZ, TU, false>), grid, dim3(kStreamThreads), 0, st, zp, ldz,
+                       up, ldu, v, chunk, S, a.labels, w.part1, w.zy);
+  return hipGetLastError();
+}
+
+template <typename TZ, typename TU, bool EMIT, bool ACCEPT>
+static hipError_t emit_dispatch(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v,
+                                const SlotArgs& a, const float* row_stats, void* dl, int64_t ldd,
+                                float* parta, int S, hipStream_t st) {
+  const TZ* zp = static_cast<const TZ*>(z);
+  const TU* up = static_cast<const TU*>(u);
+  TZ* dp = static_cast<TZ*>(dl);  // dl has the logits dtype (objective.py:80)
+  bool vec = aligned16(z) && aligned16(u) && (ldz * (int64_t)sizeof(TZ)) % 16 == 0 &&
+             (ldu * (int64_t)sizeof(TU)) % 16 == 0;
+  if (EMIT) vec = vec && aligned16(dl) && (ldd * (int64_t)sizeof(TZ)) % 16 == 0;
+  const int64_t chunk = split_chunk(v, S);
+  dim3 grid((unsigned)(S * a.n));
+  NS_TIMED(EMIT ? "stream_emit" : "stream_accept", st);
+  if (vec)
+    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, true, EMIT, ACCEPT>), grid, dim3(kStreamThreads), 0,
+                       st, zp, ldz, up, ldu, v, chunk, S, row_stats, a.labels, a.weights, a.c_ce, a.c_kl,
+                       a.inv_acc, dp, ldd, parta);
+  else
+    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, false, EMIT, ACCEPT>), grid, dim3(kStreamThreads), 0,
+                       st, zp, ldz, up, ldu, v, chunk, S, row_stats, a.labels, a.weights, a.c_ce, a.c_kl,
+                       a.inv_acc, dp, ldd, parta);
+  return hipGetLastError();
+}
+
+template <typename TZ, typename TU>
+static hipError_t forward_typed(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v,
+                                const SlotArgs& a, void* dl, int64_t ldd, float* row_stats, float* metrics,
+                                void* ws, hipStream_t st) {
+  StreamWs w;
+  stream_ws_layout(a.n, v, ws, &w);
+  const int S = stream_splits(a.n, v);
+  hipError_t e = stats_dispatch<TZ, TU>(z, ldz, u, ldu, v, a, w, S, st);
+  if (e != hipSuccess) return e;
+  if ((e = launch_merge(w.part1, w.zy, v, S, a, row_stats, st)) != hipSuccess) return e;
+  if (dl != nullptr)
+    e = emit_dispatch<TZ, TU, true, true>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, w.parta, S, st);
+  else
+    e = emit_dispatch<TZ, TU, false, true>(z, ldz, u, ldu, v, a, row_stats, nullptr, 0, w.parta, S, st);
+  if (e != hipSuccess) return e;
+  return launch_finalize(w.parta, S, a, row_stats, metrics, st);
+}
+
+hipError_t stream_forward(const void* z, int zdt, int64_t ldz, const void* u, int udt, int64_t ldu,
+                          int64_t v, const SlotArgs& a, void* dl, int64_t ldd, float* row_stats,
+                          float* metrics, void* ws, hipStream_t st) {
+  if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
+  if (zdt == kBF16 && udt == kBF16)
+    return forward_typed<uint16_t, uint16_t>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, metrics, ws, st);
+  if (zdt == kBF16 && udt == kF32)
+    return forward_typed<uint16_t, float>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, metrics, ws, st);
+  if (zdt == kF32 && udt == kBF16)
+    return forward_typed<float, uint16_t>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, metrics, ws, st);
+  return forward_typed<float, float>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, metrics, ws, st);
+}
+
+hipError_t stream_backward(const void* z, int zdt, int64_t ldz, const void* u, int udt, int64_t ldu,
+                           int64_t v, const SlotArgs& a, const float* row_stats, void* dl, int64_t ldd,
+                           hipStream_t st) {
+  if (a.n == 0) return hipSuccess;
+  const int S = stream_splits(a.n, v);
+  if (zdt == kBF16 && udt == kBF16)
+    return emit_dispatch<uint16_t, uint16_t, true, false>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, nullptr, S, st);
+  if (zdt == kBF16 && udt == kF32)
+    return emit_dispatch<uint16_t, float, true, false>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, nullptr, S, st);
+  if (zdt == kF32 && udt == kBF16)
+    return emit_dispatch<float, uint16_t, true, false>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, nullptr, S, st);
+  return emit_dispatch<float, float, true, false>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, nullptr, S, st);
+}
+
+}  // namespace ns

@@ -1,0 +1,296 @@
+"""Pins for the CPU oracle (oracle/objective_ref.py).
+
+Each check is independent of the oracle's own formulas: torch library routines
+(cross_entropy, kl_div, autograd, matmul, dtype casts), closed forms,
+known answers worked by hand, and pure-Python brute force on tiny inputs.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import objective_ref as ref
+
+
+def _logits(seed, n, v, scale=2.0, peak=6.0):
+    g = np.random.default_rng(seed)
+    z = scale * g.standard_normal((n, v))
+    z[np.arange(n), g.integers(0, v, n)] += peak
+    return z
+
+
+# --------------------------------------------------------------------- CE / KL
+
+
+def test_ce_matches_torch_cross_entropy():
+    z = _logits(0, 32, 300)
+    y = np.random.default_rng(1).integers(0, 300, 32)
+    rows = ref.row_objective(z, z * 0.5, y)
+    lib = F.cross_entropy(torch.from_numpy(z), torch.from_numpy(y), reduction="none").numpy()
+    np.testing.assert_allclose(rows["ce"], lib, rtol=1e-12, atol=1e-12)
+
+
+def test_kl_matches_torch_kl_div():
+    z, u = _logits(2, 24, 257), _logits(3, 24, 257, scale=3.0, peak=8.0)
+    y = np.zeros(24, dtype=np.int64)
+    rows = ref.row_objective(z, u, y)
+    zt, ut = torch.from_numpy(z), torch.from_numpy(u)
+    lib = F.kl_div(zt.log_softmax(-1), ut.softmax(-1), reduction="none").sum(-1).numpy()
+    np.testing.assert_allclose(rows["kl"], lib, rtol=1e-10, atol=1e-12)
+
+
+def test_constant_logits_ce_is_log_vocab_and_equal_logits_kl_zero():
+    v = 1000
+    z = np.full((3, v), 1.7)
+    rows = ref.row_objective(z, z, np.array([0, 5, 999]))
+    np.testing.assert_allclose(rows["ce"], math.log(v), rtol=1e-14)
+    np.testing.assert_allclose(rows["kl"], 0.0, atol=1e-14)
+    np.testing.assert_allclose(rows["accept_rate"], 1.0, rtol=1e-12)
+
+
+def test_accept_rate_total_variation_identity():
+    z, u = _logits(4, 16, 500), _logits(5, 16, 500, scale=3.0, peak=8.0)
+    rows = ref.row_objective(z, u, np.zeros(16, dtype=np.int64))
+    p = torch.from_numpy(z).softmax(-1)
+    t = torch.from_numpy(u).softmax(-1)
+    tv = 0.5 * (p - t).abs().sum(-1)
+    np.testing.assert_allclose(rows["accept_rate"], (1.0 - tv).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_accept_rate_brute_force_tiny():
+    g = np.random.default_rng(6)
+    z, u = g.standard_normal((3, 7)), g.standard_normal((3, 7))
+    rows = ref.row_objective(z, u, np.zeros(3, dtype=np.int64))
+    for i in range(3):
+        ez = [math.exp(x) for x in z[i]]
+        eu = [math.exp(x) for x in u[i]]
+        sz, su = sum(ez), sum(eu)
+        expect = sum(min(a / sz, b / su) for a, b in zip(ez, eu))
+        assert abs(rows["accept_rate"][i] - expect) < 1e-12
+
+
+def test_far_peaks_accept_near_zero():
+    v = 64
+    z = np.zeros((2, v))
+    u = np.zeros((2, v))
+    z[:, 3] = 60.0
+    u[:, 40] = 60.0
+    rows = ref.row_objective(z, u, np.zeros(2, dtype=np.int64))
+    assert np.all(rows["accept_rate"] < 1e-20)
+
+
+# ------------------------------------------------------------------ accept_len
+
+
+def _brute_accept(a, valid):
+    total, blocks = 0.0, 0
+    for ab, vb in zip(a, valid):
+        if not any(vb):
+            continue
+        blocks += 1
+        length, prod = 1.0, 1.0
+        for ai, vi in zip(ab, vb):
+            prod *= ai * (1.0 if vi else 0.0)
+            length += prod
+        total += length
+    return total, blocks
+
+
+def test_acceptance_known_answers():
+    valid = np.array([[1, 1, 1, 1], [1, 0, 1, 1], [0, 0, 0, 0], [1, 1, 0, 0]], dtype=bool)
+    ones = np.ones((4, 4))
+    s, tot = ref.acceptance_length_counts(ones, valid)
+    # a = 1: length = 1 + leading run of valid slots -> 5, 2, (excluded), 3
+    assert (s, tot) == (10.0, 3.0)
+    zeros = np.zeros((4, 4))
+    s, tot = ref.acceptance_length_counts(zeros, valid)
+    assert (s, tot) == (3.0, 3.0)
+    half = np.full((1, 3), 0.5)
+    s, tot = ref.acceptance_length_counts(half, np.ones((1, 3), dtype=bool))
+    assert s == pytest.approx(1 + 0.5 + 0.25 + 0.125) and tot == 1.0
+
+
+def test_acceptance_brute_force_random():
+    g = np.random.default_rng(7)
+    a = g.uniform(0, 1, (9, 5))
+    valid = g.uniform(0, 1, (9, 5)) > 0.3
+    assert ref.acceptance_length_counts(a, valid) == pytest.approx(_brute_accept(a, valid), rel=1e-14)
+
+
+def test_empty_batch_metrics():
+    v, k = 16, 4
+    z = np.zeros((2 * k, v))
+    m, _ = ref.ce_kl_loss(z, z, np.zeros((2, k)), np.zeros((2, k), dtype=np.int64), np.zeros((2, k), dtype=bool))
+    assert m["denominator"] == 0.0 and m["accept_len_total"] == 0.0
+    assert m["loss"] == 0.0 and m["accept_len"] == 0.0
+
+
+# ------------------------------------------------------------------ loss / dl
+
+
+def _library_loss(z, u, w, y, c_ce, c_kl, acc=1):
+    zt = torch.from_numpy(z).requires_grad_(True)
+    ut = torch.from_numpy(u)
+    wt = torch.from_numpy(w.astype(np.float64))
+    ce = F.cross_entropy(zt, torch.from_numpy(y), reduction="none")
+    kl = F.kl_div(zt.log_softmax(-1), ut.softmax(-1), reduction="none").sum(-1)
+    num = c_ce * (ce * wt).sum() + c_kl * (kl * wt).sum()
+    (num / acc).backward()
+    return num.item(), (ce * wt).sum().item(), (kl * wt).sum().item(), zt.grad.numpy()
+
+
+def test_loss_and_dl_match_torch_library_and_autograd():
+    n, v, k = 24, 333, 8
+    z, u = _logits(8, n, v), _logits(9, n, v, scale=3.0, peak=8.0)
+    g = np.random.default_rng(10)
+    y = g.integers(0, v, n)
+    valid = np.ones((n // k, k), dtype=bool)
+    valid[1, 5:] = False
+    w = ref.slot_weights(valid, 4.0).reshape(-1)
+    m, _ = ref.ce_kl_loss(z, u, w.reshape(-1, k), y.reshape(-1, k), valid, 0.1, 0.9)
+    num, ce_sum, kl_sum, grad = _library_loss(z, u, w, y, 0.1, 0.9, acc=3)
+    den = float(w.astype(np.float64).sum())
+    assert m["numerator"] == pytest.approx(num, rel=1e-12)
+    assert m["ce"] == pytest.approx(ce_sum / den, rel=1e-12)
+    assert m["kl"] == pytest.approx(kl_sum / den, rel=1e-12)
+    dl = ref.ce_kl_backward(z, u, w, y, 0.1, 0.9, accumulation_steps=3)
+    np.testing.assert_allclose(dl, grad, rtol=1e-9, atol=1e-15)
+
+
+def test_dl_invariants():
+    n, v = 16, 129
+    z, u = _logits(11, n, v), _logits(12, n, v)
+    y = np.random.default_rng(13).integers(0, v, n)
+    w = np.linspace(0, 1, n).astype(np.float32)
+    dl = ref.ce_kl_backward(z, u, w, y, 0.1, 0.9)
+    np.testing.assert_allclose(dl.sum(-1), 0.0, atol=1e-12)
+    assert np.all(dl[0] == 0.0)
+    dl4 = ref.ce_kl_backward(z, u, w, y, 0.1, 0.9, accumulation_steps=4)
+    np.testing.assert_allclose(dl4 * 4, dl, rtol=1e-13, atol=1e-18)
+
+
+def test_den_clamp():
+    k, v = 2, 8
+    z = np.random.default_rng(14).standard_normal((k, v))
+    w = np.full((1, k), 1e-9, dtype=np.float32)
+    m, _ = ref.ce_kl_loss(z, z, w, np.zeros((1, k), dtype=np.int64), np.ones((1, k), dtype=bool))
+    assert m["loss"] == pytest.approx(m["numerator"] / 1e-6)
+
+
+# --------------------------------------------------------------- GEMM / head
+
+
+def test_lm_head_matches_torch_matmul():
+    g = np.random.default_rng(15)
+    h, w, mk = g.standard_normal((5, 64)), 0.02 * g.standard_normal((96, 64)), g.standard_normal((5, 96))
+    z = ref.lm_head_logits(h, w, mk)
+    lib = (torch.from_numpy(h) @ torch.from_numpy(w).T + torch.from_numpy(mk)).numpy()
+    np.testing.assert_allclose(z, lib, rtol=1e-12, atol=1e-12)
+    dl = g.standard_normal((5, 96))
+    dh = ref.lm_head_backward(dl, w)
+    np.testing.assert_allclose(dh, (torch.from_numpy(dl) @ torch.from_numpy(w)).numpy(), rtol=1e-12)
+    np.testing.assert_allclose(ref.lm_head_backward(2 * dl, w), 2 * dh, rtol=1e-13)
+
+
+# --------------------------------------------------------------- formats / fp8
+
+
+def test_bf16_round_matches_torch():
+    g = np.random.default_rng(16)
+    x = (g.standard_normal(10000) * np.exp(g.uniform(-20, 20, 10000))).astype(np.float32)
+    x[:4] = [0.0, -0.0, 1e-40, 3.0e38]
+    lib = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(ref.bf16_round(x), lib)
+
+
+def test_e4m3_encode_matches_torch_cast():
+    g = np.random.default_rng(17)
+    x = np.concatenate([
+        g.uniform(-448, 448, 20000),
+        g.standard_normal(20000) * 0.01,
+        ref.E4M3_VALUES[np.isfinite(ref.E4M3_VALUES)],
+        # exact midpoints between neighbouring codes exercise ties-to-even
+        0.5 * (ref._POS_VALUES[1:] + ref._POS_VALUES[:-1]),
+    ]).astype(np.float32)
+    codes = ref.e4m3_encode(x)
+    lib = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(codes, lib)
+
+
+def test_fp8_linear_exact_on_grid_with_power_of_two_scales():
+    g = np.random.default_rng(18)
+    n, d, v = 4, 256, 128
+    finite = ref.E4M3_VALUES[np.isfinite(ref.E4M3_VALUES) & (np.abs(ref.E4M3_VALUES) <= 16)]
+    # activations: per 1x128 block, include +-448 so the dynamic scale is exactly 1
+    x = g.choice(finite, (n, d)).astype(np.float32)
+    x[:, 0], x[:, 128] = 448.0, -448.0
+    wc = ref.e4m3_encode(g.choice(finite, (v, d)))
+    scale = np.array([[2.0 ** -3, 2.0 ** 2]], dtype=np.float32)
+    out = ref.fp8_linear(x, wc, scale)
+    sw = np.repeat(np.repeat(scale, 128, 0), 128, 1)
+    exact = x.astype(np.float64) @ (ref.e4m3_decode(wc) * sw).astype(np.float64).T
+    np.testing.assert_array_equal(out, ref.bf16_round(exact.astype(np.float32)))
+
+
+def test_fp8_linear_matches_torch_float8_semantics():
+    g = np.random.default_rng(19)
+    n, d, v = 3, 256, 256
+    x = ref.bf16_round(g.standard_normal((n, d)).astype(np.float32))
+    w = (0.02 * g.standard_normal((v, d))).astype(np.float32)
+    wc, s = ref.quantize_weight_blocks(w)
+    # library restatement with torch's float8 cast
+    xt = torch.from_numpy(x)
+    xb = xt.float().reshape(n, -1, 128)
+    xs = xb.abs().amax(-1, keepdim=True) / 448.0
+    qx = (xb / xs.clamp_min(torch.finfo(torch.float32).tiny)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    dx = (qx.float() * xs).reshape(n, d)
+    wq = torch.from_numpy(wc).view(torch.float8_e4m3fn)
+    dw = (wq.float().view(v // 128, 128, d // 128, 128) * torch.from_numpy(s)[:, None, :, None]).reshape(v, d)
+    lib = (dx.double() @ dw.double().T).float().to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(ref.fp8_linear(x, wc, s), lib)
+
+
+# ------------------------------------------------------------ slot preparation
+
+
+def test_slot_preparation_known_answer():
+    ids = np.array([[10, 11, 12, 13, 14, 15]])
+    mask = np.array([[1, 1, 1, 0, 1, 1]], dtype=np.float32)
+    anchors = np.array([[0, 3, 0]])
+    keep = np.array([[True, True, False]])
+    out = ref.slot_preparation(ids, mask, anchors, keep, block_size=3, gamma=2.0)
+    # anchor 0: labels 1,2,3 -> ids 11,12,13; mask at 3 is 0 -> valid 1,1,0
+    # anchor 3: labels 4,5,6 -> 6 >= s: ids 14,15,15(clamped); valid 1,1,0
+    # not kept: safe index 0 everywhere, all invalid
+    np.testing.assert_array_equal(out["target_ids"], [[[11, 12, 13], [14, 15, 15], [10, 10, 10]]])
+    np.testing.assert_array_equal(out["valid"], [[[1, 1, 0], [1, 1, 0], [0, 0, 0]]])
+    np.testing.assert_array_equal(out["previous"], [[[10, 11, 12], [13, 14, 15], [10, 10, 10]]])
+    np.testing.assert_array_equal(out["teacher_indices"], [[0, 1, 2, 3, 4, 4, 0, 0, 0]])
+    e = math.exp(-0.5)
+    np.testing.assert_allclose(out["weights"], [[[1, e, 0], [1, e, 0], [0, 0, 0]]], rtol=1e-6)
+
+
+def test_slot_preparation_brute_force():
+    g = np.random.default_rng(20)
+    b, s, nb, k = 2, 19, 5, 4
+    ids = g.integers(0, 1000, (b, s))
+    mask = (g.uniform(0, 1, (b, s)) > 0.2).astype(np.float32)
+    anchors = g.integers(0, s, (b, nb))
+    keep = g.uniform(0, 1, (b, nb)) > 0.25
+    out = ref.slot_preparation(ids, mask, anchors, keep, k, 0.0)
+    for i in range(b):
+        for j in range(nb):
+            alive = True
+            for t in range(k):
+                label = anchors[i, j] + t + 1
+                idx = min(label, s - 1) if keep[i, j] else 0
+                assert out["target_ids"][i, j, t] == ids[i, idx]
+                alive = alive and keep[i, j] and label < s and mask[i, idx] > 0.5
+                assert out["valid"][i, j, t] == alive
+                assert out["weights"][i, j, t] == (1.0 if alive else 0.0)
+                assert out["teacher_indices"][i, j * k + t] == max(idx - 1, 0)
+                prev = ids[i, anchors[i, j]] if t == 0 else out["target_ids"][i, j, t - 1]
+                assert out["previous"][i, j, t] == prev
