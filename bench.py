@@ -33,7 +33,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c1", choices=["c1", "c2", "c3", "c4"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU-baseline sample (0: default)")
     return p.parse_args()
@@ -103,7 +103,75 @@ def workload_c1(device, args):
                 kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16")
 
 
-WORKLOADS = {"c1": workload_c1}
+# --------------------------------------------------------------------------- C2 / C3
+
+
+def workload_head(device, args, which):
+    import torch
+
+    from nanospec_amd import head, synthetic
+    from nanospec_amd.config import Objective
+
+    make = synthetic.c2 if which == "c2" else synthetic.c3
+    gamma = 4.0 if which == "c2" else 2.0
+    hidden, weight, markov, teacher, slots = make(device)
+    n, d = hidden.shape
+    v = weight.shape[0]
+    o = Objective(block_size=8, gamma=gamma)
+
+    def step():
+        metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
+        dh = head.lm_head_ce_kl_backward(saved)
+        return metrics, dh
+
+    gemm = 2.0 * n * v * d
+    kernel_flops = {"head_stats": gemm, "head_emit": gemm, "dh_gemm": gemm}
+    # byte streams of the epilogues (for the per-kernel GB/s report): pass 1 reads
+    # Markov + teacher, pass 2 also writes dl; the dh GEMM reads dl
+    kernel_bytes = {"head_stats": 4 * n * v, "head_emit": 6 * n * v, "dh_gemm": 2 * n * v}
+
+    def cpu_baseline(rows):
+        import numpy as np
+        from threadpoolctl import threadpool_info
+
+        from oracle import objective_ref as ref
+
+        rows = rows or 64
+        t_copy = time.perf_counter()
+        w32 = weight.float().cpu().numpy()
+        hs = hidden[:rows].float().cpu().numpy()
+        ms = markov[:rows].float().cpu().numpy()
+        us = teacher[:rows].float().cpu().numpy()
+        wt = slots.weights.reshape(-1)[:rows].cpu().numpy()
+        y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
+        vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
+        t_copy = time.perf_counter() - t_copy
+        t0 = time.perf_counter()
+        z = ref.lm_head_logits(hs, w32, ms, dtype=np.float32)
+        ref.ce_kl_loss(z, us, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
+                       dtype=np.float32, chunk_rows=16)
+        dl = ref.ce_kl_backward(z, us, wt, y, o.ce, o.kl, 1, dtype=np.float32).astype(np.float32)
+        ref.lm_head_backward(dl, w32, dtype=np.float32)
+        dt = time.perf_counter() - t0
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        return dict(value=rows / dt, unit="slots/s", cores=threads, kind="port",
+                    sample=f"numpy fp32 oracle (oracle/objective_ref.py): {rows} of the {n} {which.upper()} rows "
+                           f"({rows // 8} whole blocks), d={d}, V={v}: LM-head GEMM (BLAS, {threads} threads), "
+                           f"ce_kl_loss, ce_kl_backward, dh GEMM; {dt:.2f} s (weight copy {t_copy:.1f} s untimed)")
+
+    name = "C2 full fused" if which == "c2" else "C3 long-batch"
+    config = {"workload": f"{name}: LM-head GEMM + Markov addend + CE+KL+accept fwd, dl + dhidden bwd",
+              "N": n, "d": d, "V": v, "K": 8, "gamma": gamma, "global_batch": n, "seq_len": None,
+              "parallelism": "single GPU"}
+    return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d, kernel_bytes=kernel_bytes,
+                kernel_flops=kernel_flops, cpu_baseline=cpu_baseline, config=config, dtype="bf16")
+
+
+WORKLOADS = {
+    "c1": workload_c1,
+    "c2": lambda dev, a: workload_head(dev, a, "c2"),
+    "c3": lambda dev, a: workload_head(dev, a, "c3"),
+}
 
 
 def main():

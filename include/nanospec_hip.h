@@ -80,6 +80,30 @@ int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, 
                         float c_kl, float inv_acc, const float* row_stats, void* dl, int64_t ldd,
                         ns_stream_t stream);
 
+/* Fused LM head + objective forward (train.py:272-279 -> objective.py:49-67):
+ * z = hidden . weight^T (+ markov) is formed tile by tile on bf16 MFMA and never
+ * stored; pass 1 folds (max, sum-exp) of z and the teacher row and A = sum t(u - z);
+ * pass 2 recomputes z and emits the accept rate and, when dl is not NULL,
+ * dl = (w * inv_acc)[(c_ce + c_kl) p - c_kl t - c_ce e_y] as bf16.
+ * hidden [N, d] bf16, weight [V, d] bf16 (the frozen LM head), markov [N, V] bf16
+ * or NULL, teacher [N, V] (t_dtype), dl [N, V] bf16 or NULL.
+ * Requires d % 64 == 0, V % 8 == 0, 16-byte aligned rows, n % k == 0. */
+int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
+                        const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
+                        float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
+                        float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+
+/* LM-head backward dh = dl . weight (train.py:302): dl [N, V] bf16, weight [V, d]
+ * bf16, dh [N, d] bf16.  Split-K over V with a fixed-order fp32 reduction. */
+int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
+                  int64_t n, int64_t v, int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+
+/* Plain LM-head projection out = x . weight^T (+ addend), bf16 out (ops.py:34-35 for
+ * the head: train.py:272, 279, 284).  x [N, d], weight [V, d], addend [N, V] or NULL. */
+int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
+                     int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, ns_stream_t stream);
+
 /* ---- timing instrumentation (opt-in) -------------------------------------
  * Between ns_profile_begin() and ns_profile_end(), every kernel the library
  * launches is bracketed by HIP events recorded on its launch stream.

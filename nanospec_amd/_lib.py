@@ -42,8 +42,14 @@ SIGNATURES = {
         [_P, _I, _I64, _P, _I, _I64, _P, _P, _I64, _I64, _F, _F, _F, _P, _P, _I64, _P],
         _I,
     ),
+    "ns_lmhead_ce_kl_fwd": (
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F,
+         _P, _I64, _P, _P, _P, _SZ, _P],
+        _I,
+    ),
+    "ns_lmhead_bwd": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
+    "ns_lmhead_linear": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], _I),
 }
-
 
 
 class KernelTime(ctypes.Structure):

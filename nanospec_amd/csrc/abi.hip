@@ -24,6 +24,8 @@ int hip_status(hipError_t e, const char* where) {
 
 bool dtype_ok(int dt) { return dt == NS_BF16 || dt == NS_F32; }
 
+bool aligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 int check_slots(const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n, int64_t k,
                 bool need_valid) {
   if (n < 0) return fail(NS_EINVAL, "n must be >= 0 (got %lld)", (long long)n);
@@ -55,6 +57,10 @@ size_t ns_workspace_bytes(int kind, int64_t n, int64_t v, int64_t d) {
   switch (kind) {
     case NS_WS_LOGITS:
       return ns::stream_workspace_bytes(n, v);
+    case NS_WS_LMHEAD:
+      return ns::lmhead_workspace_bytes(n, v, d);
+    case NS_WS_LMHEAD_BWD:
+      return ns::lmhead_bwd_workspace_bytes(n, v, d);
     default:
       return 0;
   }
@@ -102,6 +108,74 @@ int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, 
   return hip_status(ns::stream_backward(z, z_dtype, ldz, u, u_dtype, ldu, v, a, row_stats, dl, ldd,
                                         reinterpret_cast<hipStream_t>(stream)),
                     "ns_ce_kl_logits_bwd");
+}
+
+int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
+                        const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
+                        float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
+                        float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+  if (!dtype_ok(t_dtype)) return fail(NS_EDTYPE, "unsupported teacher dtype code %d", t_dtype);
+  if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
+  if (d < 64 || d % 64) return fail(NS_EINVAL, "hidden size must be a positive multiple of 64 (got %lld)", (long long)d);
+  int rc;
+  if ((rc = check_slots(labels, weights, valid, n, k, true))) return rc;
+  if ((rc = check_matrix(hidden, n, d, ldh, "hidden"))) return rc;
+  if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
+  if (markov && (rc = check_matrix(markov, n, v, ldm, "markov"))) return rc;
+  if ((rc = check_matrix(teacher, n, v, ldt, "teacher"))) return rc;
+  if (dl && (rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
+  if (!metrics || (n > 0 && !row_stats)) return fail(NS_ENULL, "metrics and row_stats must be non-NULL");
+  const int64_t tq = t_dtype == NS_BF16 ? 8 : 4;
+  if (!aligned(hidden) || !aligned(weight) || !aligned(teacher) || (markov && !aligned(markov)) || (dl && !aligned(dl)) ||
+      ldh % 8 || ldw % 8 || (markov && ldm % 8) || ldt % tq || (dl && ldd % 8))
+    return fail(NS_EALIGN, "fused head needs 16-byte aligned base pointers and rows");
+  const size_t need = ns::lmhead_workspace_bytes(n, v, d);
+  if (n > 0 && (!workspace || workspace_bytes < need))
+    return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  ns::SlotArgs a{labels, weights, valid, n, k, c_ce, c_kl, inv_acc};
+  return hip_status(ns::lmhead_forward(hidden, ldh, weight, ldw, markov, ldm, teacher, t_dtype, ldt, d, v, a, dl, ldd,
+                                       row_stats, metrics, workspace, reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_ce_kl_fwd");
+}
+
+int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
+                  int64_t n, int64_t v, int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
+  if (d < 8 || d % 8) return fail(NS_EINVAL, "hidden size must be a positive multiple of 8 (got %lld)", (long long)d);
+  int rc;
+  if ((rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
+  if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
+  if ((rc = check_matrix(dh, n, d, lddh, "dh"))) return rc;
+  if (!aligned(dl) || !aligned(weight) || !aligned(dh) || ldd % 8 || ldw % 8 || lddh % 4)
+    return fail(NS_EALIGN, "dh GEMM needs 16-byte aligned base pointers and rows");
+  const size_t need = ns::lmhead_bwd_workspace_bytes(n, v, d);
+  if (n > 0 && (!workspace || workspace_bytes < need))
+    return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  return hip_status(ns::lmhead_backward(dl, ldd, weight, ldw, dh, lddh, n, v, d, workspace,
+                                        reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_bwd");
+}
+
+int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
+                     int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
+  if (d < 64 || d % 64) return fail(NS_EINVAL, "hidden size must be a positive multiple of 64 (got %lld)", (long long)d);
+  int rc;
+  if ((rc = check_matrix(x, n, d, ldx, "x"))) return rc;
+  if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
+  if (addend && (rc = check_matrix(addend, n, v, lda, "addend"))) return rc;
+  if ((rc = check_matrix(out, n, v, ldo, "out"))) return rc;
+  if (!aligned(x) || !aligned(weight) || !aligned(out) || (addend && !aligned(addend)) || ldx % 8 || ldw % 8 ||
+      ldo % 8 || (addend && lda % 8))
+    return fail(NS_EALIGN, "linear needs 16-byte aligned base pointers and rows");
+  return hip_status(ns::lmhead_linear(x, ldx, weight, ldw, addend, lda, out, ldo, n, v, d,
+                                      reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_linear");
 }
 
 }  // extern "C"

@@ -1,0 +1,725 @@
+// Fused LM head + draft objective on bf16 MFMA (gfx950, v_mfma_f32_32x32x16_bf16).
+//
+// Forward (nanospec/train.py:272-279 + objective.py:49-67), never storing logits:
+//   z^T tile = W_lm[v-tile] . hidden[t-tile]^T   (vocab on the MFMA M axis, tokens on N)
+//   pass 1 ("stats"): epilogue adds the Markov tile, reads the teacher tile and folds
+//     (max, sum-exp) of z and u plus A = sum exp(u - m_u)(u - z) into per-token running
+//     state kept in registers across the workgroup's vocab range -> RowPart partials;
+//     the lane that owns (token, label) writes z_label.
+//   merge (shared with the logits path): LSE_z, LSE_u, CE, KL per token.
+//   pass 2 ("emit"): recomputes the z tile, p = exp(z - LSE_z), t = exp(u - LSE_u),
+//     accumulates sum min(p, t) and writes dl = (w/acc)[(c_ce + c_kl) p - c_kl t - c_ce e_y]
+//     as bf16.
+// Backward (train.py:302): dh = dl . W_lm as a long-K (K = V) split-K MFMA GEMM with a
+// fixed-order fp32 reduction of the split partials.
+//
+// Layout choices (MI355X): one 256-thread workgroup per CU (4 waves, 2 x 2, each a
+// 128 x 128 accumulator tile = 256 AGPRs/lane), 256 x 256 x 64 LDS stages double
+// buffered with an XOR swizzle on 16-byte chunks, persistent workgroups that walk a
+// contiguous vocab range with per-token running statistics, and a workgroup -> tile map
+// that puts the workgroups sharing a W stream on the same XCD (shared L2).
+#include "ns_internal.h"
+#include "ns_profile.h"
+
+namespace ns {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) char lds_t;   // LDS byte pointer
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int BM = 256;          // MFMA rows per workgroup tile
+constexpr int BN = 256;          // MFMA columns per workgroup tile
+constexpr int BK = 64;           // K per LDS stage
+constexpr int kThreads = 256;    // 4 waves as 2 (M) x 2 (N), 128 x 128 each
+constexpr int kStageBytes = BM * BK * 2;    // 32 KB per operand per stage
+constexpr int kGemmLds = 4 * kStageBytes;   // 2 stages x 2 operands = 128 KB
+constexpr int kZRow = BM + 4;               // padded fp32 row of the epilogue dump
+constexpr int kDumpLds = 128 * kZRow * 4;   // 128 token rows x 256 vocab fp32
+constexpr int kLdsBytes = kGemmLds > kDumpLds ? kGemmLds : kDumpLds;
+constexpr int kNumXcd = 8;
+
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte chunk swizzle: rows r and r+8 rotate, so 8- and 16-lane groups reading one
+// logical chunk of consecutive rows hit distinct banks.
+__device__ __forceinline__ int swz(int row) { return ((row & 7) + ((row >> 3) & 1)) & 7; }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ swz(row)) << 4); }
+
+// Per-lane byte offsets of a 256 (rows) x 64 (K) bf16 tile of a K-contiguous matrix,
+// relative to the uniform address of element (r0, k0).  Thread t loads rows
+// i*32 + t/8 (i = 0..7), 16-byte chunk t%8; rows >= rmax are clamped (never used).
+struct RowTile {
+  uint32_t off[8];
+  __device__ __forceinline__ void init(int64_t ld, int64_t r0, int64_t rmax) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int64_t row = r0 + i * 32 + (tid >> 3);
+      row = row < rmax ? row : rmax - 1;
+      off[i] = (uint32_t)(((row - r0) * ld + (tid & 7) * 8) * 2);
+    }
+  }
+  __device__ __forceinline__ void load(uint4 (&v)[8], const char* base) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint4*>(base + off[i]);
+  }
+  // Stage with only `kvalid` (< BK) valid K entries: the rest reads chunk 0 and is zeroed.
+  __device__ __forceinline__ void load_tail(uint4 (&v)[8], const char* base, int kvalid) const {
+    const int c = (threadIdx.x & 7) * 8;
+    const bool ok = c < kvalid;
+    const uint32_t back = ok ? 0u : (uint32_t)(c * 2);
+    const uint32_t keep = ok ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 x = *reinterpret_cast<const uint4*>(base + off[i] - back);
+      x.x &= keep; x.y &= keep; x.z &= keep; x.w &= keep;
+      v[i] = x;
+    }
+  }
+};
+
+__device__ __forceinline__ void store_tile(const uint4 (&v)[8], lds_t* lds) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = i * 32 + (tid >> 3);
+    const u32x4_t y = {v[i].x, v[i].y, v[i].z, v[i].w};
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(lds + lds_off(row, tid & 7)) = y;
+  }
+}
+
+// Per-lane offsets of a 64 (K rows) x 256 (columns) bf16 tile of a row-major [K, cols]
+// matrix that is transposed into the [col][K] swizzled LDS layout.  Thread t handles the
+// (4-row, 8-column) groups t and t + 256; columns >= cmax are clamped (never used).
+struct ColTile {
+  uint32_t off[2];
+  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int grp = threadIdx.x + h * kThreads;
+      const int rg = grp >> 5, cg = grp & 31;
+      int64_t col = c0 + cg * 8;
+      col = col < cmax ? col : cmax - 8;
+      off[h] = (uint32_t)(((int64_t)rg * 4 * ld + (col - c0)) * 2);
+    }
+  }
+  __device__ __forceinline__ void load(uint4 (&v)[2][4], const char* base, int64_t ld_bytes) const {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[h][j] = *reinterpret_cast<const uint4*>(base + off[h] + j * ld_bytes);
+  }
+  __device__ __forceinline__ void load_tail(uint4 (&v)[2][4], const char* base, int64_t ld_bytes, int kvalid) const {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rg = (threadIdx.x + h * kThreads) >> 5;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = rg * 4 + j < kvalid;
+        const uint32_t keep = ok ? 0xffffffffu : 0u;
+        uint4 x = *reinterpret_cast<const uint4*>(base + (ok ? off[h] + j * ld_bytes : 0));
+        x.x &= keep; x.y &= keep; x.z &= keep; x.w &= keep;
+        v[h][j] = x;
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ void store_tile_t(const uint4 (&v)[2][4], lds_t* lds) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int grp = threadIdx.x + h * kThreads;
+    const int rg = grp >> 5, cg = grp & 31;
+    const uint32_t w[4][4] = {{v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w},
+                              {v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w},
+                              {v[h][2].x, v[h][2].y, v[h][2].z, v[h][2].w},
+                              {v[h][3].x, v[h][3].y, v[h][3].z, v[h][3].w}};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int sh = (c & 1) * 16;
+      const uint32_t e0 = (w[0][c >> 1] >> sh) & 0xffffu;
+      const uint32_t e1 = (w[1][c >> 1] >> sh) & 0xffffu;
+      const uint32_t e2 = (w[2][c >> 1] >> sh) & 0xffffu;
+      const uint32_t e3 = (w[3][c >> 1] >> sh) & 0xffffu;
+      const int row = cg * 8 + c;
+      const int off = lds_off(row, rg >> 1) + (rg & 1) * 8;
+      const u32x2_t y = {e0 | (e1 << 16), e2 | (e3 << 16)};
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + off) = y;
+    }
+  }
+}
+
+// One BK stage of MFMAs for this wave's 128 x 128 block.
+__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la, const lds_t* lb) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 31, kh = lane >> 5;
+#pragma unroll
+  for (int kk = 0; kk < BK / 16; ++kk) {
+    bf16x8_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+          la + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
+      b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+          lb + lds_off(wn * 128 + i * 32 + r, kk * 2 + kh));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[4][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+}
+
+// acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T, both row-major with K contiguous and
+// K a multiple of BK.  Ends with a barrier (LDS free for the caller).
+__device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
+                                        int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
+                                        int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
+  const int KT = (int)(K / BK);
+  RowTile ta, tb;
+  ta.init(lda, a0, amax);
+  tb.init(ldb, b0, bmax);
+  const char* pa = reinterpret_cast<const char*>(A + a0 * lda);
+  const char* pb = reinterpret_cast<const char*>(B + b0 * ldb);
+  uint4 ra[8], rb[8];
+  ta.load(ra, pa);
+  tb.load(rb, pb);
+  store_tile(ra, lds);
+  store_tile(rb, lds + kStageBytes);
+  __syncthreads();
+  if (KT > 1) {
+    ta.load(ra, pa + BK * 2);
+    tb.load(rb, pb + BK * 2);
+  }
+  for (int kt = 0; kt < KT; ++kt) {
+    lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
+    lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
+    mma_stage(acc, cur, cur + kStageBytes);
+    if (kt + 1 < KT) {
+      store_tile(ra, nxt);
+      store_tile(rb, nxt + kStageBytes);
+    }
+    __syncthreads();
+    if (kt + 2 < KT) {
+      ta.load(ra, pa + (int64_t)(kt + 2) * BK * 2);
+      tb.load(rb, pb + (int64_t)(kt + 2) * BK * 2);
+    }
+  }
+}
+
+// acc += A[a0:a0+256, k0:k1] . B[k0:k1, c0:c0+256] with A row-major (K contiguous) and
+// B row-major [K, cols] (columns contiguous, transposed through LDS).  Entries with
+// K >= kmax are zero.  Ends with a barrier.
+__device__ __forceinline__ void gemm_nn(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
+                                        int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
+                                        int64_t c0, int64_t cmax, int64_t k0, int64_t k1, int64_t kmax,
+                                        lds_t* lds) {
+  const int KT = (int)((k1 - k0 + BK - 1) / BK);
+  if (KT <= 0) return;
+  RowTile ta;
+  ColTile tb;
+  ta.init(lda, a0, amax);
+  tb.init(ldb, c0, cmax);
+  const int64_t ldb_bytes = ldb * 2;
+  const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
+  const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
+  uint4 ra[8], rb[2][4];
+  auto load_stage = [&](int kt) {
+    const int64_t kvalid = kmax - (k0 + (int64_t)kt * BK);
+    const char* a = pa + (int64_t)kt * BK * 2;
+    const char* b = pb + (int64_t)kt * BK * ldb_bytes;
+    if (kvalid >= BK) {
+      ta.load(ra, a);
+      tb.load(rb, b, ldb_bytes);
+    } else {
+      ta.load_tail(ra, a, (int)kvalid);
+      tb.load_tail(rb, b, ldb_bytes, (int)kvalid);
+    }
+  };
+  load_stage(0);
+  store_tile(ra, lds);
+  store_tile_t(rb, lds + kStageBytes);
+  __syncthreads();
+  if (KT > 1) load_stage(1);
+  for (int kt = 0; kt < KT; ++kt) {
+    lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
+    lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
+    mma_stage(acc, cur, cur + kStageBytes);
+    if (kt + 1 < KT) {
+      store_tile(ra, nxt);
+      store_tile_t(rb, nxt + kStageBytes);
+    }
+    __syncthreads();
+    if (kt + 2 < KT) load_stage(kt + 2);
+  }
+}
+
+// Waves holding token columns [128 * half, 128 * half + 128) write their fp32 block to
+// LDS as zt[token][vocab] (row kZRow floats).  Caller guarantees wn == half.
+__device__ __forceinline__ void dump_half(const f32x16_t (&acc)[4][4], lds_t* lds) {
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
+  const int r = lane & 31, h = lane >> 5;
+  lds_f32* zt = reinterpret_cast<lds_f32*>(lds);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int tl = j * 32 + r;
+        const int vr = wm * 128 + i * 32 + 8 * g + 4 * h;
+        const f32x4_t x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        *reinterpret_cast<__attribute__((address_space(3))) f32x4_t*>(zt + tl * kZRow + vr) = x;
+      }
+}
+
+// Workgroup -> (token tile, vocab split) map.  Workgroups are dispatched round-robin over
+// the 8 XCDs; logical ids are laid out so that each XCD holds consecutive ids, and
+// consecutive ids share a vocab split (the W stream) across token tiles.
+__device__ __forceinline__ void wg_coords(int g, int G, int TT, int& t, int& s) {
+  int L = g;
+  if (G % kNumXcd == 0) L = (g % kNumXcd) * (G / kNumXcd) + g / kNumXcd;
+  s = L / TT;
+  t = L % TT;
+}
+
+// ------------------------------------------------------------------ head kernel
+
+struct HeadParams {
+  const uint16_t* hidden;   // [N, d] bf16
+  const uint16_t* weight;   // [V, d] bf16
+  const uint16_t* markov;   // [N, V] bf16 or null
+  const void* teacher;      // [N, V] bf16 / f32
+  int64_t ldh, ldw, ldm, ldt;
+  int64_t n, d, v;
+  int tt, vt, splits;       // token tiles, vocab tiles, vocab splits
+  const int64_t* labels;
+  const float* weights;
+  float c_ce, c_kl, inv_acc;
+  const float* row_stats;   // pass 2 input
+  RowPart* part1;           // pass 1 output [N][splits]
+  float* zy;                // pass 1 output [N]
+  float* parta;             // pass 2 output [N][splits]
+  uint16_t* dl;             // pass 2 output [N, V] bf16 or null
+  int64_t ldd;
+  uint16_t* out;            // MODE_STORE output [N, V] bf16
+  int64_t ldo;
+};
+
+enum { MODE_STATS = 0, MODE_EMIT = 1, MODE_STORE = 2 };
+
+// Objective epilogue for one token row over this thread's vocab range [vs, vs + nval)
+// of the current tile: zr points at the dumped fp32 logits (LDS), nval is a multiple
+// of 8 (V % 8 == 0).
+template <int MODE, typename TT>
+__device__ __forceinline__ void epilogue_row(const HeadParams& p, const lds_f32* zr, int64_t t, bool tok_ok,
+                                             int64_t vs, int nval, int64_t y, PairState& st, float& arate,
+                                             float lzl, float lul, float cp, float ct, float cy) {
+  if (nval <= 0) return;
+  const uint16_t* mrow = p.markov ? p.markov + t * p.ldm + vs : nullptr;
+  const TT* urow = static_cast<const TT*>(p.teacher) + t * p.ldt + vs;
+  for (int e = 0; e < nval; e += 16) {
+    const bool second = e + 8 < nval;
+    float z[16], u[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4_t x = *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(zr + e + 4 * q);
+      z[4 * q] = x[0]; z[4 * q + 1] = x[1]; z[4 * q + 2] = x[2]; z[4 * q + 3] = x[3];
+    }
+    if (mrow) {
+      float mk[16];
+      load8(mrow + e, mk);
+      if (second) load8(mrow + e + 8, mk + 8);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) z[q] += (q < 8 || second) ? mk[q] : 0.f;
+    }
+    if (MODE == MODE_STORE) {
+      if (tok_ok) {
+        store8(p.out + t * p.ldo + vs + e, z);
+        if (second) store8(p.out + t * p.ldo + vs + e + 8, z + 8);
+      }
+      continue;
+    }
+    load8(urow + e, u);
+    if (second) {
+      load8(urow + e + 8, u + 8);
+    } else {
+#pragma unroll
+      for (int q = 8; q < 16; ++q) { z[q] = kNegBig; u[q] = kNegBig; }
+    }
+    if (MODE == MODE_STATS) {
+      pair_update<16>(st, z, u);
+    } else {
+      float d[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const float pp = fast_exp2(__builtin_fmaf(z[q], kLog2e, -lzl));
+        const float tt = fast_exp2(__builtin_fmaf(u[q], kLog2e, -lul));
+        arate += fminf(pp, tt);
+        d[q] = __builtin_fmaf(cp, pp, -ct * tt);
+      }
+      if (p.dl && tok_ok) {
+        store8(p.dl + t * p.ldd + vs + e, d);
+        if (second) store8(p.dl + t * p.ldd + vs + e + 8, d + 8);
+      }
+    }
+  }
+  if (MODE == MODE_STORE) return;
+  // the label entry: pass 1 records z_y, pass 2 rewrites dl[y] with the -c_ce term
+  const int64_t yr = y - vs;
+  if (yr >= 0 && yr < nval && tok_ok) {
+    const float zy = zr[yr] + (mrow ? bf16_to_f32(mrow[yr]) : 0.f);
+    if (MODE == MODE_STATS) {
+      p.zy[t] = zy;
+    } else if (p.dl) {
+      const float uy = load1(urow + yr);
+      const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
+      const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
+      store1(p.dl + t * p.ldd + vs + yr, __builtin_fmaf(cp, pp, -ct * tt) - cy);
+    }
+  }
+}
+
+template <int MODE, typename TT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void head_kernel(HeadParams p) {
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  lds_t* lds = (lds_t*)lds_raw;
+  lds_f32* zt = reinterpret_cast<lds_f32*>(lds);
+  int tile_t, split;
+  wg_coords(blockIdx.x, gridDim.x, p.tt, tile_t, split);
+  const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
+  const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
+  const int tid = threadIdx.x;
+  const int wn = (tid >> 6) & 1;
+  const int tl = tid & 127, hh = tid >> 7;   // epilogue: token row in the half, vocab half
+  const int64_t t0 = (int64_t)tile_t * BN;
+
+  // this thread's two epilogue tokens (one per 128-token half) and their constants
+  int64_t trow[2], ylab[2] = {0, 0};
+  bool tok_ok[2];
+  PairState st[2];
+  float arate[2] = {0.f, 0.f};
+  float lzl[2] = {0.f, 0.f}, lul[2] = {0.f, 0.f}, cp[2] = {0.f, 0.f}, ct[2] = {0.f, 0.f}, cy[2] = {0.f, 0.f};
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int64_t t = t0 + jj * 128 + tl;
+    tok_ok[jj] = t < p.n;
+    trow[jj] = tok_ok[jj] ? t : p.n - 1;
+    st[jj] = pair_init();
+    if (MODE != MODE_STORE) ylab[jj] = p.labels[trow[jj]];
+    if (MODE == MODE_EMIT) {
+      lzl[jj] = p.row_stats[trow[jj] * kRowStatWidth + kLseZ] * kLog2e;
+      lul[jj] = p.row_stats[trow[jj] * kRowStatWidth + kLseU] * kLog2e;
+      const float w = p.weights[trow[jj]] * p.inv_acc;
+      cp[jj] = w * (p.c_ce + p.c_kl);
+      ct[jj] = w * p.c_kl;
+      cy[jj] = w * p.c_ce;
+    }
+  }
+
+  f32x16_t acc[4][4];
+  for (int vt = vt_begin; vt < vt_end; ++vt) {
+    const int64_t v0 = (int64_t)vt * BM;
+    zero_acc(acc);
+    gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds);
+    const int64_t vs = v0 + hh * 128;
+    const int64_t rem = p.v - vs;
+    const int nval = rem >= 128 ? 128 : (rem > 0 ? (int)rem : 0);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      if (wn == jj) dump_half(acc, lds);
+      __syncthreads();
+      epilogue_row<MODE, TT>(p, zt + tl * kZRow + hh * 128, trow[jj], tok_ok[jj], vs, nval, ylab[jj], st[jj],
+                             arate[jj], lzl[jj], lul[jj], cp[jj], ct[jj], cy[jj]);
+      __syncthreads();
+    }
+  }
+
+  if (MODE == MODE_STORE) return;
+  // combine the two vocab halves of every token and write this split's partial
+  lds_f32* red = zt;   // [2 halves][256 tokens][5]
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    lds_f32* dst = red + (hh * 256 + jj * 128 + tl) * 5;
+    if (MODE == MODE_STATS) {
+      dst[0] = st[jj].mz; dst[1] = st[jj].sz; dst[2] = st[jj].mu; dst[3] = st[jj].su; dst[4] = st[jj].A;
+    } else {
+      dst[0] = arate[jj];
+    }
+  }
+  __syncthreads();
+  const int64_t t = t0 + tid;
+  if (t < p.n) {
+    const lds_f32* a = red + tid * 5;
+    const lds_f32* b = red + (256 + tid) * 5;
+    if (MODE == MODE_STATS) {
+      const PairState r = pair_merge(PairState{a[0], a[1], a[2], a[3], a[4]},
+                                     PairState{b[0], b[1], b[2], b[3], b[4]});
+      RowPart rp;
+      rp.mz = r.mz; rp.sz = r.sz; rp.mu = r.mu; rp.su = r.su; rp.A = r.A;
+      rp.pad0 = rp.pad1 = rp.pad2 = 0.f;
+      p.part1[t * p.splits + split] = rp;
+    } else {
+      p.parta[t * p.splits + split] = a[0] + b[0];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dh = dl . W kernel
+
+struct BwdParams {
+  const uint16_t* dl;      // [N, V] bf16
+  const uint16_t* weight;  // [V, d] bf16
+  int64_t ldd, ldw;
+  int64_t n, v, d;
+  int mt, ct, ksplit;      // token tiles, d tiles, K splits
+  int kt_total;            // ceil(V / BK)
+  float* part;             // [ksplit][N][d] fp32
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void dh_kernel(BwdParams p) {
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  lds_t* lds = (lds_t*)lds_raw;
+  // Tile order: consecutive workgroups share a K split and a d tile (W stream) across
+  // token tiles; XCD-aware like the forward.
+  const int G = gridDim.x;
+  int L = blockIdx.x;
+  if (G % kNumXcd == 0) L = (L % kNumXcd) * (G / kNumXcd) + L / kNumXcd;
+  const int mt = L % p.mt;
+  const int rest = L / p.mt;
+  const int ct = rest % p.ct;
+  const int ks = rest / p.ct;
+  const int kt0 = (int)((int64_t)ks * p.kt_total / p.ksplit);
+  const int kt1 = (int)((int64_t)(ks + 1) * p.kt_total / p.ksplit);
+  const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)ct * BN;
+  f32x16_t acc[4][4];
+  zero_acc(acc);
+  gemm_nn(acc, p.dl, p.ldd, m0, p.n, p.weight, p.ldw, c0, p.d, (int64_t)kt0 * BK, (int64_t)kt1 * BK, p.v, lds);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int h = lane >> 5;
+  float* out = p.part + (int64_t)ks * p.n * p.d;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = c0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+        if (row < p.n && col < p.d) out[row * p.d + col] = acc[i][j][e];
+      }
+    }
+}
+
+__global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict__ part, int ksplit, int64_t n,
+                                                        int64_t d, uint16_t* __restrict__ dh, int64_t lddh) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int64_t total = n * d;
+  if (idx >= total) return;
+  const int64_t row = idx / d, col = idx % d;
+  float4 s = *reinterpret_cast<const float4*>(part + idx);
+  for (int k = 1; k < ksplit; ++k) {
+    const float4 x = *reinterpret_cast<const float4*>(part + (int64_t)k * total + idx);
+    s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+  }
+  uint2 o;
+  o.x = pack_bf16x2(s.x, s.y);
+  o.y = pack_bf16x2(s.z, s.w);
+  *reinterpret_cast<uint2*>(dh + row * lddh + col) = o;
+}
+
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+struct HeadPlan {
+  int tt, vt, splits, grid;
+};
+
+HeadPlan head_plan(int64_t n, int64_t v) {
+  HeadPlan pl;
+  pl.tt = (int)((n + BN - 1) / BN);
+  pl.vt = (int)((v + BM - 1) / BM);
+  const int cus = device_cus();
+  int s = (cus + pl.tt - 1) / pl.tt;
+  if (s < 1) s = 1;
+  if (s > pl.vt) s = pl.vt;
+  pl.splits = s;
+  pl.grid = pl.tt * s;
+  return pl;
+}
+
+struct HeadWs {
+  RowPart* part1;
+  float* parta;
+  float* zy;
+};
+
+size_t head_ws_layout(int64_t n, int64_t v, void* base, HeadWs* out) {
+  const HeadPlan pl = head_plan(n, v);
+  const size_t b1 = align_up((size_t)n * pl.splits * sizeof(RowPart), 256);
+  const size_t b2 = align_up((size_t)n * pl.splits * sizeof(float), 256);
+  const size_t b3 = align_up((size_t)n * sizeof(float), 256);
+  if (out) {
+    char* c = static_cast<char*>(base);
+    out->part1 = reinterpret_cast<RowPart*>(c);
+    out->parta = reinterpret_cast<float*>(c + b1);
+    out->zy = reinterpret_cast<float*>(c + b1 + b2);
+  }
+  return b1 + b2 + b3;
+}
+
+struct BwdPlan {
+  int mt, ct, ksplit, kt_total, grid;
+};
+
+BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d) {
+  BwdPlan pl;
+  pl.mt = (int)((n + BM - 1) / BM);
+  pl.ct = (int)((d + BN - 1) / BN);
+  pl.kt_total = (int)((v + BK - 1) / BK);
+  const int tiles = pl.mt * pl.ct;
+  const int cus = device_cus();
+  int ks = (4 * cus + tiles - 1) / tiles;
+  if (ks < 1) ks = 1;
+  if (ks > 16) ks = 16;
+  if (ks > pl.kt_total) ks = pl.kt_total;
+  pl.ksplit = ks;
+  pl.grid = tiles * ks;
+  return pl;
+}
+
+template <int MODE, typename TT>
+hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char* name) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<MODE, TT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  NS_TIMED(name, st);
+  hipLaunchKernelGGL((head_kernel<MODE, TT>), dim3(grid), dim3(kThreads), kLdsBytes, st, p);
+  return hipGetLastError();
+}
+
+template <typename TT>
+hipError_t head_forward_typed(HeadParams& p, const HeadPlan& pl, const SlotArgs& a, float* row_stats,
+                              float* metrics, const HeadWs& w, hipStream_t st) {
+  hipError_t e = launch_head<MODE_STATS, TT>(p, pl.grid, st, "head_stats");
+  if (e != hipSuccess) return e;
+  if ((e = launch_merge(w.part1, w.zy, p.v, pl.splits, a, row_stats, st)) != hipSuccess) return e;
+  p.row_stats = row_stats;
+  if ((e = launch_head<MODE_EMIT, TT>(p, pl.grid, st, "head_emit")) != hipSuccess) return e;
+  return launch_finalize(w.parta, pl.splits, a, row_stats, metrics, st);
+}
+
+}  // namespace
+
+size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d) {
+  (void)d;
+  return head_ws_layout(n, v, nullptr, nullptr);
+}
+
+hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                          int64_t ldm, const void* teacher, int tdt, int64_t ldt, int64_t d, int64_t v,
+                          const SlotArgs& a, void* dl, int64_t ldd, float* row_stats, float* metrics, void* ws,
+                          hipStream_t st) {
+  if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
+  const HeadPlan pl = head_plan(a.n, v);
+  HeadWs w;
+  head_ws_layout(a.n, v, ws, &w);
+  HeadParams p = {};
+  p.hidden = static_cast<const uint16_t*>(hidden);
+  p.weight = static_cast<const uint16_t*>(weight);
+  p.markov = static_cast<const uint16_t*>(markov);
+  p.teacher = teacher;
+  p.ldh = ldh; p.ldw = ldw; p.ldm = ldm; p.ldt = ldt;
+  p.n = a.n; p.d = d; p.v = v;
+  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits;
+  p.labels = a.labels; p.weights = a.weights;
+  p.c_ce = a.c_ce; p.c_kl = a.c_kl; p.inv_acc = a.inv_acc;
+  p.part1 = w.part1; p.zy = w.zy; p.parta = w.parta;
+  p.dl = static_cast<uint16_t*>(dl); p.ldd = ldd;
+  if (tdt == kBF16) return head_forward_typed<uint16_t>(p, pl, a, row_stats, metrics, w, st);
+  return head_forward_typed<float>(p, pl, a, row_stats, metrics, w, st);
+}
+
+size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d) {
+  const BwdPlan pl = bwd_plan(n, v, d);
+  return align_up((size_t)pl.ksplit * n * d * sizeof(float), 256);
+}
+
+hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
+                           int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st) {
+  if (n == 0 || d == 0) return hipSuccess;
+  const BwdPlan pl = bwd_plan(n, v, d);
+  BwdParams p = {};
+  p.dl = static_cast<const uint16_t*>(dl);
+  p.weight = static_cast<const uint16_t*>(weight);
+  p.ldd = ldd; p.ldw = ldw; p.n = n; p.v = v; p.d = d;
+  p.mt = pl.mt; p.ct = pl.ct; p.ksplit = pl.ksplit; p.kt_total = pl.kt_total;
+  p.part = static_cast<float*>(ws);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dh_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  {
+    NS_TIMED("dh_gemm", st);
+    hipLaunchKernelGGL(dh_kernel, dim3(pl.grid), dim3(kThreads), kLdsBytes, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const int64_t quads = (n * d + 3) / 4;
+  NS_TIMED("dh_reduce", st);
+  hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p.part, pl.ksplit,
+                     n, d, static_cast<uint16_t*>(dh), lddh);
+  return hipGetLastError();
+}
+
+hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
+                         int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, hipStream_t st) {
+  if (n == 0 || v == 0) return hipSuccess;
+  const HeadPlan pl = head_plan(n, v);
+  HeadParams p = {};
+  p.hidden = static_cast<const uint16_t*>(x);
+  p.weight = static_cast<const uint16_t*>(weight);
+  p.markov = static_cast<const uint16_t*>(addend);
+  p.ldh = ldx; p.ldw = ldw; p.ldm = lda;
+  p.n = n; p.d = d; p.v = v;
+  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits;
+  p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
+  p.teacher = nullptr;
+  return launch_head<MODE_STORE, uint16_t>(p, pl.grid, st, "head_linear");
+}
+
+}  // namespace ns

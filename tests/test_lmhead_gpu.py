@@ -1,0 +1,182 @@
+"""GPU parity of the fused LM-head path (ns_lmhead_ce_kl_fwd, ns_lmhead_bwd,
+ns_lmhead_linear) against the CPU oracle.
+
+Tolerances (north star): loss, ce, kl, accept_len within 1e-4 relative of the
+fp32 objective; the label pick exact in index; dhidden max error <= 2e-2 of
+max|dh| and cosine >= 0.9999; dl within one bf16 ulp plus fp32 evaluation error.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from nanospec_amd import head, synthetic
+from nanospec_amd.config import Objective
+from oracle import objective_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+FIELDS = ("ce", "kl", "numerator", "denominator", "accept_len_sum", "accept_len_total")
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _metrics(m):
+    out = {f: float(getattr(m, f)) for f in FIELDS}
+    out["loss"] = float(m.loss)
+    out["accept_len"] = float(m.accept_len)
+    return out
+
+
+def _assert_metrics(got, want, rel=1e-4):
+    for key in FIELDS + ("loss", "accept_len"):
+        w = want[key]
+        assert got[key] == pytest.approx(w, rel=rel, abs=1e-6 * max(1.0, abs(w))), (key, got[key], w)
+
+
+def _assert_dl(dl_gpu, dl_ref):
+    diff = np.abs(dl_gpu.astype(np.float64) - dl_ref)
+    scale = np.abs(dl_ref).max(axis=-1, keepdims=True)
+    tol = np.abs(dl_ref) * 2.0 ** -7 + 2e-5 * scale
+    assert np.all(diff <= tol), float((diff - tol).max())
+
+
+def _assert_dh(dh_gpu, dh_ref):
+    sim = ref.similarity(dh_gpu, dh_ref)
+    assert sim["cosine"] >= 0.9999, sim
+    assert sim["max_abs"] <= 2e-2 * np.abs(dh_ref).max(), sim
+
+
+def _oracle_head(hidden, weight, markov, teacher, slots, o, rows=None, dtype=np.float64):
+    """Oracle z, metrics, rows, dl and dh on whole blocks `rows` (default all)."""
+    h, w = _np(hidden), _np(weight)
+    mk = _np(markov) if markov is not None else None
+    u = _np(teacher)
+    wt = _np(slots.weights).reshape(-1)
+    y = slots.target_ids.reshape(-1).cpu().numpy()
+    valid = slots.valid.cpu().numpy()
+    k = valid.shape[-1]
+    if rows is not None:
+        h, u, wt, y = h[rows], u[rows], wt[rows], y[rows]
+        mk = mk[rows] if mk is not None else None
+        valid = valid.reshape(-1)[rows].reshape(-1, k)
+    z = ref.lm_head_logits(h, w, mk, dtype=dtype)
+    m, r = ref.ce_kl_loss(z, u, wt.reshape(-1, k), y.reshape(-1, k), valid, o.ce, o.kl)
+    dl = ref.ce_kl_backward(z, u, wt, y, o.ce, o.kl)
+    dh = ref.lm_head_backward(dl, w, dtype=dtype)
+    return z, m, r, dl, dh
+
+
+def _run(hidden, weight, markov, teacher, slots, o):
+    m, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
+    dh, dl = head.lm_head_ce_kl_backward(saved, return_dlogits=True)
+    torch.cuda.synchronize()
+    return m, saved, dh, dl
+
+
+def _check_full(hidden, weight, markov, teacher, slots, o):
+    m, saved, dh, dl = _run(hidden, weight, markov, teacher, slots, o)
+    z, m_ref, rows, dl_ref, dh_ref = _oracle_head(hidden, weight, markov, teacher, slots, o)
+    _assert_metrics(_metrics(m), m_ref)
+    rs = _np(saved.row_stats)
+    np.testing.assert_allclose(rs[:, 0], rows["lse_z"], rtol=2e-6, atol=5e-5)
+    np.testing.assert_allclose(rs[:, 1], rows["lse_u"], rtol=2e-6, atol=5e-5)
+    np.testing.assert_allclose(rs[:, 4], rows["accept_rate"], atol=1e-5)
+    n = z.shape[0]
+    y = slots.target_ids.reshape(-1).cpu().numpy()
+    np.testing.assert_allclose(rs[:, 5], z[np.arange(n), y], rtol=1e-5, atol=1e-5)
+    _assert_dl(_np(dl).reshape(n, -1), dl_ref)
+    _assert_dh(_np(dh).reshape(n, -1), dh_ref)
+    return m, dh, dl
+
+
+def test_c0_full_oracle(gpu_lib):
+    hidden, weight, markov, teacher, slots = synthetic.c0(DEV)
+    _check_full(hidden, weight, markov, teacher, slots, Objective(block_size=8))
+
+
+@pytest.mark.parametrize("n,d,v", [
+    (72, 128, 8200),     # partial token tile, partial vocab tile, V % 64 != 0 (dh K tail)
+    (264, 192, 2056),    # two token tiles, one vocab tile plus a sliver
+    (512, 64, 16384),    # several vocab splits
+])
+def test_odd_shapes(gpu_lib, n, d, v):
+    hidden, weight, markov, teacher, slots = synthetic.head_inputs(n, d, v, 77 + n, DEV)
+    _check_full(hidden, weight, markov, teacher, slots, Objective(block_size=8))
+
+
+def test_fp32_teacher_no_markov_ragged(gpu_lib):
+    hidden, weight, _, teacher, slots = synthetic.head_inputs(128, 256, 4096, 91, DEV, ragged=True, gamma=2.0)
+    _check_full(hidden, weight, None, teacher.float(), slots, Objective(block_size=8, gamma=2.0))
+
+
+def test_linear_matches_oracle(gpu_lib):
+    hidden, weight, markov, _, _ = synthetic.head_inputs(72, 128, 8200, 5, DEV)
+    out = head.lm_head_linear(hidden, weight, markov)
+    plain = head.lm_head_linear(hidden, weight)
+    torch.cuda.synchronize()
+    z = ref.lm_head_logits(_np(hidden), _np(weight), _np(markov))
+    z0 = ref.lm_head_logits(_np(hidden), _np(weight))
+    # bf16 output: within one bf16 ulp of the exact fp32 result (+ accumulation error)
+    for got, want in ((out, z), (plain, z0)):
+        g = _np(got)
+        assert np.all(np.abs(g - want) <= np.abs(want) * 2.0 ** -7 + 1e-4), float(np.abs(g - want).max())
+
+
+def test_dh_gemm_alone(gpu_lib):
+    g = torch.Generator(device=DEV).manual_seed(3)
+    n, v, d = 300, 8200, 320
+    dl = (1e-3 * torch.randn((n, v), generator=g, device=DEV)).bfloat16()
+    w = (0.02 * torch.randn((v, d), generator=g, device=DEV)).bfloat16()
+    dh = head.lm_head_linear_backward(dl, w)
+    torch.cuda.synchronize()
+    _assert_dh(_np(dh), ref.lm_head_backward(_np(dl), _np(w)))
+
+
+def test_deterministic(gpu_lib):
+    hidden, weight, markov, teacher, slots = synthetic.head_inputs(256, 256, 8192, 8, DEV)
+    o = Objective(block_size=8)
+    m1, _, dh1, dl1 = _run(hidden, weight, markov, teacher, slots, o)
+    m2, _, dh2, dl2 = _run(hidden, weight, markov, teacher, slots, o)
+    assert torch.equal(dl1, dl2) and torch.equal(dh1, dh2)
+    for f in FIELDS:
+        assert torch.equal(getattr(m1, f), getattr(m2, f))
+
+
+def _check_large(hidden, weight, markov, teacher, slots, o, blocks):
+    m, saved, dh, dl = _run(hidden, weight, markov, teacher, slots, o)
+    rs = _np(saved.row_stats)
+    wt = _np(slots.weights).reshape(-1).astype(np.float64)
+    valid = slots.valid.cpu().numpy()
+    got = _metrics(m)
+    den = wt.sum()
+    assert got["denominator"] == pytest.approx(den, rel=1e-6)
+    assert got["ce"] == pytest.approx((wt * rs[:, 2]).sum() / den, rel=1e-5)
+    assert got["kl"] == pytest.approx((wt * rs[:, 3]).sum() / den, rel=1e-5)
+    s, tot = ref.acceptance_length_counts(rs[:, 4].reshape(-1, 8), valid)
+    assert got["accept_len_sum"] == pytest.approx(s, rel=1e-5) and got["accept_len_total"] == tot
+    k = 8
+    rows = np.concatenate([np.arange(b * k, b * k + k) for b in blocks])
+    z, m_ref, r, dl_ref, dh_ref = _oracle_head(hidden, weight, markov, teacher, slots, o, rows=rows,
+                                               dtype=np.float32)
+    np.testing.assert_allclose(rs[rows, 0], r["lse_z"], rtol=5e-6, atol=1e-4)
+    np.testing.assert_allclose(rs[rows, 2], r["ce"], rtol=2e-5, atol=1e-4)
+    np.testing.assert_allclose(rs[rows, 3], r["kl"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(rs[rows, 4], r["accept_rate"], atol=2e-5)
+    _assert_dl(_np(dl.reshape(-1, dl.shape[-1])[rows]), dl_ref)
+    _assert_dh(_np(dh.reshape(-1, dh.shape[-1])[rows]), dh_ref)
+
+
+def test_c2_full_size(gpu_lib):
+    """C2: N = 4096, d = 5120, V = 248,320 (whole-block oracle + metric consistency)."""
+    hidden, weight, markov, teacher, slots = synthetic.c2(DEV)
+    _check_large(hidden, weight, markov, teacher, slots, Objective(block_size=8), blocks=(0, 301))
+
+
+def test_c3_full_size(gpu_lib):
+    """C3: N = 32,768, ragged prefix masks, gamma = 2."""
+    hidden, weight, markov, teacher, slots = synthetic.c3(DEV)
+    _check_large(hidden, weight, markov, teacher, slots, Objective(block_size=8, gamma=2.0), blocks=(5, 4000))

@@ -46,8 +46,10 @@ def _assert_dl_bf16(dl_gpu, dl_ref):
     correctly rounded value itself."""
     exact = ref.bf16_round(dl_ref.astype(np.float32))
     diff = np.abs(dl_gpu.astype(np.float64) - dl_ref)
-    ulp = np.abs(dl_ref) * 2.0 ** -7 + 1e-30
-    assert np.all(diff <= ulp + 1e-12), float((diff - ulp).max())
+    # one bf16 ulp, plus fp32-evaluation error where (c_ce+c_kl) p and c_kl t cancel
+    scale = np.abs(dl_ref).max(axis=-1, keepdims=True)
+    tol = np.abs(dl_ref) * 2.0 ** -7 + 1e-6 * scale
+    assert np.all(diff <= tol), float((diff - tol).max())
     assert np.mean(dl_gpu == exact) > 0.999
 
 
