@@ -104,6 +104,16 @@ int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, 
 int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                      int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, ns_stream_t stream);
 
+/* Objective inputs of every draft slot from sampled anchors (dspark.py:116-127, 143):
+ * ids [b, s] int64, loss_mask [b, s] fp32, anchors [b, nb] int64 (each in [0, s)),
+ * keep [b, nb] uint8 -> target_ids, previous [b, nb, k] int64, weights [b, nb, k]
+ * fp32 (valid * exp(-slot / gamma); no decay when gamma <= 0), valid [b, nb, k]
+ * uint8 (prefix product), teacher_indices [b, nb * k] int64.  s >= 1. */
+int ns_prepare_slots(const int64_t* ids, const float* loss_mask, const int64_t* anchors, const uint8_t* keep,
+                     int64_t b, int64_t s, int64_t nb, int64_t k, float gamma, int64_t* target_ids,
+                     int64_t* previous, float* weights, uint8_t* valid, int64_t* teacher_indices,
+                     ns_stream_t stream);
+
 /* ---- timing instrumentation (opt-in) -------------------------------------
  * Between ns_profile_begin() and ns_profile_end(), every kernel the library
  * launches is bracketed by HIP events recorded on its launch stream.

@@ -49,6 +49,7 @@ SIGNATURES = {
     ),
     "ns_lmhead_bwd": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "ns_lmhead_linear": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], _I),
+    "ns_prepare_slots": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _P], _I),
 }
 
 

@@ -178,4 +178,19 @@ int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw
                     "ns_lmhead_linear");
 }
 
+int ns_prepare_slots(const int64_t* ids, const float* loss_mask, const int64_t* anchors, const uint8_t* keep,
+                     int64_t b, int64_t s, int64_t nb, int64_t k, float gamma, int64_t* target_ids,
+                     int64_t* previous, float* weights, uint8_t* valid, int64_t* teacher_indices,
+                     ns_stream_t stream) {
+  if (s < 1) return fail(NS_EINVAL, "Empty input sequence");
+  if (b < 0 || nb < 0) return fail(NS_EINVAL, "batch and block counts must be >= 0");
+  if (k < 1) return fail(NS_EINVAL, "block_size must be positive");
+  if (b * nb > 0 && (!ids || !loss_mask || !anchors || !keep || !target_ids || !previous || !weights || !valid ||
+                     !teacher_indices))
+    return fail(NS_ENULL, "every tensor argument must be non-NULL");
+  return hip_status(ns::prepare_slots(ids, loss_mask, anchors, keep, b, s, nb, k, gamma, target_ids, previous,
+                                      weights, valid, teacher_indices, reinterpret_cast<hipStream_t>(stream)),
+                    "ns_prepare_slots");
+}
+
 }  // extern "C"

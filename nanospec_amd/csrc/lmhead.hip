@@ -334,6 +334,11 @@ __device__ __forceinline__ void epilogue_row(const HeadParams& p, const lds_f32*
   if (nval <= 0) return;
   const uint16_t* mrow = p.markov ? p.markov + t * p.ldm + vs : nullptr;
   const TT* urow = static_cast<const TT*>(p.teacher) + t * p.ldt + vs;
+  // Sums over this tile's (at most 128) entries are formed locally and folded into the
+  // running state once per tile: a single running fp32 sum over a whole vocab range
+  // (up to ~10^5 terms per lane) would lose the many small terms to rounding.
+  PairState loc = pair_init();
+  float aloc = 0.f;
   for (int e = 0; e < nval; e += 16) {
     const bool second = e + 8 < nval;
     float z[16], u[16];
@@ -364,14 +369,14 @@ __device__ __forceinline__ void epilogue_row(const HeadParams& p, const lds_f32*
       for (int q = 8; q < 16; ++q) { z[q] = kNegBig; u[q] = kNegBig; }
     }
     if (MODE == MODE_STATS) {
-      pair_update<16>(st, z, u);
+      pair_update<16>(loc, z, u);
     } else {
       float d[16];
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const float pp = fast_exp2(__builtin_fmaf(z[q], kLog2e, -lzl));
         const float tt = fast_exp2(__builtin_fmaf(u[q], kLog2e, -lul));
-        arate += fminf(pp, tt);
+        aloc += fminf(pp, tt);
         d[q] = __builtin_fmaf(cp, pp, -ct * tt);
       }
       if (p.dl && tok_ok) {
@@ -381,6 +386,8 @@ __device__ __forceinline__ void epilogue_row(const HeadParams& p, const lds_f32*
     }
   }
   if (MODE == MODE_STORE) return;
+  if (MODE == MODE_STATS) st = pair_merge(st, loc);
+  else arate += aloc;
   // the label entry: pass 1 records z_y, pass 2 rewrites dl[y] with the -c_ce term
   const int64_t yr = y - vs;
   if (yr >= 0 && yr < nval && tok_ok) {
