@@ -80,7 +80,7 @@ def workload_c1(device, args):
 
         from oracle import objective_ref as ref
 
-        rows = rows or 256
+        rows = rows or n
         zs = z[:rows].float().cpu().numpy()
         us = u[:rows].float().cpu().numpy()
         w = slots.weights.reshape(-1)[:rows].cpu().numpy()
@@ -136,7 +136,7 @@ def workload_head(device, args, which):
 
         from oracle import objective_ref as ref
 
-        rows = rows or 64
+        rows = rows or 1024
         t_copy = time.perf_counter()
         w32 = weight.float().cpu().numpy()
         hs = hidden[:rows].float().cpu().numpy()

@@ -104,6 +104,21 @@ int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, 
 int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                      int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, ns_stream_t stream);
 
+/* Teacher logits from a block-FP8 head with ops.fp8_linear numerics (ops.py:183-200):
+ * x [N, d] bf16 is quantised per 1x128 block (scale amax/448, e4m3 round-to-nearest-
+ * even), wq [V, d] holds e4m3 codes with one fp32 scale per 128x128 block in
+ * scale [V/128, d/128] (the scale multiplies); out [N, V] bf16 = bf16 of the fp32
+ * sum over K blocks of x_scale * w_scale * (fp8 dot product on MFMA).
+ * Requires V % 128 == 0 and d % 128 == 0 (ValueError in the reference). */
+int ns_fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const float* scale,
+                          void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, void* workspace,
+                          size_t workspace_bytes, ns_stream_t stream);
+
+/* The activation half of the above alone: q [N, d] e4m3 codes (row stride d) and
+ * xs [N, d/128] fp32 scales of x [N, d] bf16 (ops.py:189-196). */
+int ns_fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs,
+                         ns_stream_t stream);
+
 /* Objective inputs of every draft slot from sampled anchors (dspark.py:116-127, 143):
  * ids [b, s] int64, loss_mask [b, s] fp32, anchors [b, nb] int64 (each in [0, s)),
  * keep [b, nb] uint8 -> target_ids, previous [b, nb, k] int64, weights [b, nb, k]

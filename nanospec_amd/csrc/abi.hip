@@ -61,6 +61,8 @@ size_t ns_workspace_bytes(int kind, int64_t n, int64_t v, int64_t d) {
       return ns::lmhead_workspace_bytes(n, v, d);
     case NS_WS_LMHEAD_BWD:
       return ns::lmhead_bwd_workspace_bytes(n, v, d);
+    case NS_WS_FP8:
+      return ns::fp8_workspace_bytes(n, d);
     default:
       return 0;
   }
@@ -176,6 +178,38 @@ int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw
   return hip_status(ns::lmhead_linear(x, ldx, weight, ldw, addend, lda, out, ldo, n, v, d,
                                       reinterpret_cast<hipStream_t>(stream)),
                     "ns_lmhead_linear");
+}
+
+int ns_fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const float* scale,
+                          void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, void* workspace,
+                          size_t workspace_bytes, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (v < 128 || v % 128 || d < 128 || d % 128) return fail(NS_EINVAL, "Expected checkpoint's 128x128 FP8 weight blocks");
+  int rc;
+  if ((rc = check_matrix(x, n, d, ldx, "x"))) return rc;
+  if ((rc = check_matrix(wq, v, d, ldw, "wq"))) return rc;
+  if ((rc = check_matrix(out, n, v, ldo, "out"))) return rc;
+  if (!scale) return fail(NS_ENULL, "scale is NULL");
+  if (!aligned(x) || !aligned(wq) || !aligned(out) || ldx % 8 || ldw % 16 || ldo % 4)
+    return fail(NS_EALIGN, "fp8 head needs 16-byte aligned base pointers and rows");
+  const size_t need = ns::fp8_workspace_bytes(n, d);
+  if (n > 0 && (!workspace || workspace_bytes < need))
+    return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  return hip_status(ns::fp8_teacher_logits(x, ldx, wq, ldw, scale, out, ldo, n, v, d, workspace,
+                                           reinterpret_cast<hipStream_t>(stream)),
+                    "ns_fp8_teacher_logits");
+}
+
+int ns_fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs,
+                         ns_stream_t stream) {
+  if (n < 0 || d < 128 || d % 128) return fail(NS_EINVAL, "d must be a positive multiple of 128");
+  int rc;
+  if ((rc = check_matrix(x, n, d, ldx, "x"))) return rc;
+  if (n > 0 && (!q || !xs)) return fail(NS_ENULL, "q and xs must be non-NULL");
+  if ((reinterpret_cast<uintptr_t>(x) & 3u) || ldx % 2) return fail(NS_EALIGN, "x rows must be 4-byte aligned");
+  return hip_status(ns::fp8_quantize_rows(x, ldx, n, d, q, xs, reinterpret_cast<hipStream_t>(stream)),
+                    "ns_fp8_quantize_rows");
 }
 
 int ns_prepare_slots(const int64_t* ids, const float* loss_mask, const int64_t* anchors, const uint8_t* keep,

@@ -53,6 +53,8 @@ hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t
 
 // ---- FP8 teacher head (fp8.hip) ---------------------------------------------
 size_t fp8_workspace_bytes(int64_t n, int64_t d);
+hipError_t fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs,
+                             hipStream_t st);
 hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw,
                               const float* scale, void* out, int64_t ldo, int64_t n, int64_t v,
                               int64_t d, void* ws, hipStream_t st);
