@@ -112,20 +112,32 @@ def workload_head(device, args, which):
     from nanospec_amd import head, synthetic
     from nanospec_amd.config import Objective
 
-    make = synthetic.c2 if which == "c2" else synthetic.c3
-    gamma = 4.0 if which == "c2" else 2.0
-    hidden, weight, markov, teacher, slots = make(device)
+    gamma = 2.0 if which == "c3" else 4.0
+    fp8 = None
+    if which == "c4":
+        from nanospec_amd import ops
+
+        hidden, weight, markov, fp8, slots = synthetic.c4(device)
+        teacher = None
+    else:
+        make = synthetic.c2 if which == "c2" else synthetic.c3
+        hidden, weight, markov, teacher, slots = make(device)
     n, d = hidden.shape
     v = weight.shape[0]
     o = Objective(block_size=8, gamma=gamma)
 
     def step():
-        metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
+        u = teacher
+        if fp8 is not None:
+            xt, codes, scale = fp8
+            u = ops.fp8_linear(xt, codes.view(torch.float8_e4m3fn), scale)
+        metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, u, slots, o, markov_logits=markov)
         dh = head.lm_head_ce_kl_backward(saved)
         return metrics, dh
 
     gemm = 2.0 * n * v * d
     kernel_flops = {"head_stats": gemm, "head_emit": gemm, "dh_gemm": gemm}
+    kernel_fp8_flops = {"fp8_head_gemm": gemm} if fp8 is not None else {}
     # byte streams of the epilogues (for the per-kernel GB/s report): pass 1 reads
     # Markov + teacher, pass 2 also writes dl; the dh GEMM reads dl
     kernel_bytes = {"head_stats": 4 * n * v, "head_emit": 6 * n * v, "dh_gemm": 2 * n * v}
@@ -141,12 +153,20 @@ def workload_head(device, args, which):
         w32 = weight.float().cpu().numpy()
         hs = hidden[:rows].float().cpu().numpy()
         ms = markov[:rows].float().cpu().numpy()
-        us = teacher[:rows].float().cpu().numpy()
+        if fp8 is not None:
+            xt, codes, scale = fp8
+            xq = xt[:rows].float().cpu().numpy()
+            wc = codes.cpu().numpy()
+            sc = scale.cpu().numpy()
+        else:
+            us = teacher[:rows].float().cpu().numpy()
         wt = slots.weights.reshape(-1)[:rows].cpu().numpy()
         y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
         vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
         t_copy = time.perf_counter() - t_copy
         t0 = time.perf_counter()
+        if fp8 is not None:
+            us = ref.fp8_linear(xq, wc, sc, dtype=np.float32)
         z = ref.lm_head_logits(hs, w32, ms, dtype=np.float32)
         ref.ce_kl_loss(z, us, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
                        dtype=np.float32, chunk_rows=16)
@@ -159,18 +179,21 @@ def workload_head(device, args, which):
                            f"({rows // 8} whole blocks), d={d}, V={v}: LM-head GEMM (BLAS, {threads} threads), "
                            f"ce_kl_loss, ce_kl_backward, dh GEMM; {dt:.2f} s (weight copy {t_copy:.1f} s untimed)")
 
-    name = "C2 full fused" if which == "c2" else "C3 long-batch"
+    name = {"c2": "C2 full fused", "c3": "C3 long-batch", "c4": "C4 FP8 teacher head + full fused"}[which]
     config = {"workload": f"{name}: LM-head GEMM + Markov addend + CE+KL+accept fwd, dl + dhidden bwd",
               "N": n, "d": d, "V": v, "K": 8, "gamma": gamma, "global_batch": n, "seq_len": None,
               "parallelism": "single GPU"}
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d, kernel_bytes=kernel_bytes,
-                kernel_flops=kernel_flops, cpu_baseline=cpu_baseline, config=config, dtype="bf16")
+                kernel_flops=kernel_flops, kernel_fp8_flops=kernel_fp8_flops, cpu_baseline=cpu_baseline,
+                config=config, dtype="bf16" if fp8 is None else "bf16+fp8",
+                per_slot_fp8_flops=2.0 * v * d if fp8 is not None else None)
 
 
 WORKLOADS = {
     "c1": workload_c1,
     "c2": lambda dev, a: workload_head(dev, a, "c2"),
     "c3": lambda dev, a: workload_head(dev, a, "c3"),
+    "c4": lambda dev, a: workload_head(dev, a, "c4"),
 }
 
 
@@ -234,18 +257,27 @@ def main():
     roof["kernel"] = dominant
     roof["kernel_mean_ms"] = dom_ms
     roof["traffic"] = None
+    fp8_flops = wl.get("kernel_fp8_flops", {})
     for name, info in kernels.items():
         if name in wl["kernel_bytes"]:
             info["algorithmic_GBs"] = wl["kernel_bytes"][name] / (info["mean_ms"] / 1e3) / 1e9
         if name in wl["kernel_flops"]:
             info["algorithmic_TFLOPs"] = wl["kernel_flops"][name] / (info["mean_ms"] / 1e3) / 1e12
+            info["mfma_frac"] = info["algorithmic_TFLOPs"] / BF16_PEAK_TFLOPS
+        if name in fp8_flops:
+            info["algorithmic_TFLOPs"] = fp8_flops[name] / (info["mean_ms"] / 1e3) / 1e12
+            info["mfma_frac_fp8"] = info["algorithmic_TFLOPs"] / FP8_PEAK_TFLOPS
     step_roof = {}
     if wl["per_slot_bytes"]:
         step_roof["algorithmic_GBs"] = wl["per_slot_bytes"] * n / (ms_per_step / 1e3) / 1e9
         step_roof["hbm_frac"] = step_roof["algorithmic_GBs"] / HBM_PEAK_GBS
     if wl["per_slot_flops"]:
         step_roof["algorithmic_TFLOPs"] = wl["per_slot_flops"] * n / (ms_per_step / 1e3) / 1e12
-        step_roof["mfma_frac"] = step_roof["algorithmic_TFLOPs"] / BF16_PEAK_TFLOPS
+        # time the step would take at the dense peaks, over the measured step time
+        ideal_s = wl["per_slot_flops"] * n / (BF16_PEAK_TFLOPS * 1e12)
+        if wl.get("per_slot_fp8_flops"):
+            ideal_s += wl["per_slot_fp8_flops"] * n / (FP8_PEAK_TFLOPS * 1e12)
+        step_roof["mfma_frac"] = ideal_s / (ms_per_step / 1e3)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -153,28 +153,48 @@ __device__ __forceinline__ void store_tile_t(const uint4 (&v)[2][4], lds_t* lds)
   }
 }
 
-// One BK stage of MFMAs for this wave's 128 x 128 block.
-__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la, const lds_t* lb) {
+// MFMA operand fragments of one 16-wide K step for this wave's 128 x 128 block.
+struct Frags {
+  bf16x8_t a[4], b[4];
+};
+
+__device__ __forceinline__ void load_frags(Frags& f, const lds_t* la, const lds_t* lb, int kk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int r = lane & 31, kh = lane >> 5;
 #pragma unroll
-  for (int kk = 0; kk < BK / 16; ++kk) {
-    bf16x8_t a[4], b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-          la + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
-      b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-          lb + lds_off(wn * 128 + i * 32 + r, kk * 2 + kh));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  for (int i = 0; i < 4; ++i) {
+    f.a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+        la + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
+    f.b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+        lb + lds_off(wn * 128 + i * 32 + r, kk * 2 + kh));
   }
+}
+
+__device__ __forceinline__ void mma_frags(f32x16_t (&acc)[4][4], const Frags& f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+// One BK stage (four 16-wide K steps): fragments of step k+1 load while the 16 MFMAs
+// of step k run; `mid` (the next stage's LDS stores and global prefetch) is issued
+// after the second step so that it overlaps the remaining MFMAs.
+template <typename Mid>
+__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la, const lds_t* lb, Mid&& mid) {
+  Frags f0, f1;
+  load_frags(f0, la, lb, 0);
+  load_frags(f1, la, lb, 1);
+  mma_frags(acc, f0);
+  load_frags(f0, la, lb, 2);
+  mma_frags(acc, f1);
+  mid();
+  load_frags(f1, la, lb, 3);
+  mma_frags(acc, f0);
+  mma_frags(acc, f1);
 }
 
 __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[4][4]) {
@@ -210,16 +230,17 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
   for (int kt = 0; kt < KT; ++kt) {
     lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
     lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
-    mma_stage(acc, cur, cur + kStageBytes);
-    if (kt + 1 < KT) {
-      store_tile(ra, nxt);
-      store_tile(rb, nxt + kStageBytes);
-    }
+    mma_stage(acc, cur, cur + kStageBytes, [&]() {
+      if (kt + 1 < KT) {
+        store_tile(ra, nxt);
+        store_tile(rb, nxt + kStageBytes);
+      }
+      if (kt + 2 < KT) {
+        ta.load(ra, pa + (int64_t)(kt + 2) * BK * 2);
+        tb.load(rb, pb + (int64_t)(kt + 2) * BK * 2);
+      }
+    });
     __syncthreads();
-    if (kt + 2 < KT) {
-      ta.load(ra, pa + (int64_t)(kt + 2) * BK * 2);
-      tb.load(rb, pb + (int64_t)(kt + 2) * BK * 2);
-    }
   }
 }
 
@@ -260,13 +281,14 @@ __device__ __forceinline__ void gemm_nn(f32x16_t (&acc)[4][4], const uint16_t* _
   for (int kt = 0; kt < KT; ++kt) {
     lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
     lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
-    mma_stage(acc, cur, cur + kStageBytes);
-    if (kt + 1 < KT) {
-      store_tile(ra, nxt);
-      store_tile_t(rb, nxt + kStageBytes);
-    }
+    mma_stage(acc, cur, cur + kStageBytes, [&]() {
+      if (kt + 1 < KT) {
+        store_tile(ra, nxt);
+        store_tile_t(rb, nxt + kStageBytes);
+      }
+      if (kt + 2 < KT) load_stage(kt + 2);
+    });
     __syncthreads();
-    if (kt + 2 < KT) load_stage(kt + 2);
   }
 }
 

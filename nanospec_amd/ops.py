@@ -1,0 +1,74 @@
+"""Ops of the reference's head path (nanospec/ops.py), on HIP.
+
+* ``ce_kl_loss`` / ``ce_kl_backward``: re-exported as in ops.py:12.
+* ``linear(x, weight)``: the LM-head projection (ops.py:34-35 as called at
+  train.py:272, 279 and 284) on the bf16 MFMA tiles; bf16 in and out.
+* ``lm_head_backward(dl, weight)``: ``dl @ lm_head.w`` (train.py:302).
+* ``fp8_linear(x, weight, scale)``: block-FP8 projection with ops.py:183-200
+  numerics; a non-fp8 weight takes the bf16 ``linear`` path as in the reference.
+
+No CPU fallback: unsupported dtypes or shapes raise ``ValueError``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from nanospec_amd import _lib
+from nanospec_amd.head import lm_head_linear, lm_head_linear_backward
+from nanospec_amd.objective import ce_kl_backward as ce_kl_backward  # noqa: F401
+from nanospec_amd.objective import ce_kl_loss as ce_kl_loss  # noqa: F401
+
+
+def linear(x, weight, bias=None):
+    if bias is not None:
+        raise ValueError("the LM-head projection has no bias")
+    return lm_head_linear(x, weight)
+
+
+def lm_head_backward(dl, weight):
+    return lm_head_linear_backward(dl, weight)
+
+
+@torch.no_grad()
+def fp8_linear(x, weight, scale):
+    """Reference quantisation, expanded scales, fp32 accumulation, bf16 output."""
+    if weight.dtype != torch.float8_e4m3fn:
+        return linear(x, weight)
+    v, d = weight.shape
+    if v % 128 or d % 128:
+        raise ValueError("Expected checkpoint's 128x128 FP8 weight blocks")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"fp8_linear activations must be bfloat16 (got {x.dtype})")
+    device = _lib.require_device(x, weight, scale)
+    xr, ldx = _lib.rows_2d(x, d)
+    wq = weight.view(torch.uint8)
+    wr, ldw = _lib.rows_2d(wq, d)
+    sc = scale.to(torch.float32).contiguous()
+    if tuple(sc.shape) != (v // 128, d // 128):
+        raise ValueError(f"scale must be [{v // 128}, {d // 128}] (got {tuple(sc.shape)})")
+    n = xr.shape[0]
+    out = torch.empty((n, v), dtype=torch.bfloat16, device=device)
+    ws = _lib.workspace(_lib.NS_WS_FP8, n, v, d, device)
+    status = _lib.load().ns_fp8_teacher_logits(
+        _lib.ptr(xr), ldx, _lib.ptr(wr), ldw, _lib.ptr(sc), _lib.ptr(out), v, n, v, d,
+        _lib.ptr(ws), ws.numel(), _lib.stream(device),
+    )
+    _lib.check(status, "ns_fp8_teacher_logits")
+    return out.view(tuple(x.shape[:-1]) + (v,))
+
+
+@torch.no_grad()
+def fp8_quantize_rows(x):
+    """(codes uint8 [N, d], scales fp32 [N, d/128]) of the 1x128 activation
+    quantisation of ops.py:189-196."""
+    n_rows = x.numel() // x.shape[-1]
+    d = x.shape[-1]
+    device = _lib.require_device(x)
+    xr, ldx = _lib.rows_2d(x, d)
+    q = torch.empty((n_rows, d), dtype=torch.uint8, device=device)
+    xs = torch.empty((n_rows, d // 128), dtype=torch.float32, device=device)
+    status = _lib.load().ns_fp8_quantize_rows(_lib.ptr(xr), ldx, n_rows, d, _lib.ptr(q), _lib.ptr(xs),
+                                              _lib.stream(device))
+    _lib.check(status, "ns_fp8_quantize_rows")
+    return q, xs
