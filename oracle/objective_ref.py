@@ -350,16 +350,25 @@ def fp8_linear(x, weight_codes, scale, dtype=np.float64):
 
 
 def similarity(actual, expected) -> dict:
-    a = np.asarray(actual, dtype=np.float64).reshape(-1)
-    e = np.asarray(expected, dtype=np.float64).reshape(-1)
+    """Row cosine (min and mean over rows of the last axis), whole-tensor cosine,
+    relative L2 and max |diff| -- the comparison metrics of experiments/compare.py:80-89."""
+    a2 = np.asarray(actual, dtype=np.float64)
+    e2 = np.asarray(expected, dtype=np.float64)
+    a2 = a2.reshape(-1, a2.shape[-1]) if a2.ndim else a2.reshape(1, 1)
+    e2 = e2.reshape(-1, e2.shape[-1]) if e2.ndim else e2.reshape(1, 1)
+    dots = (a2 * e2).sum(-1)
+    norms = np.linalg.norm(a2, axis=-1) * np.linalg.norm(e2, axis=-1)
+    row_cos = dots / np.maximum(norms, 1e-300)
+    a, e = a2.reshape(-1), e2.reshape(-1)
     na, ne = np.linalg.norm(a), np.linalg.norm(e)
     cos = float(a @ e / (na * ne)) if na > 0 and ne > 0 else float("nan")
     diff = a - e
     return dict(
         cosine=cos,
+        cosine_min=float(row_cos.min()),
+        cosine_mean=float(row_cos.mean()),
         relative_l2=float(np.linalg.norm(diff) / max(ne, 1e-30)),
         max_abs=float(np.abs(diff).max()) if diff.size else 0.0,
-        max_rel=float((np.abs(diff) / np.maximum(np.abs(e), 1e-30)).max()) if diff.size else 0.0,
     )
 
 

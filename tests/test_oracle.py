@@ -294,3 +294,14 @@ def test_slot_preparation_brute_force():
                 assert out["teacher_indices"][i, j * k + t] == max(idx - 1, 0)
                 prev = ids[i, anchors[i, j]] if t == 0 else out["target_ids"][i, j, t - 1]
                 assert out["previous"][i, j, t] == prev
+
+
+def test_similarity_metrics():
+    a = np.array([[1.0, 0.0], [0.0, 2.0]])
+    e = np.array([[1.0, 0.0], [2.0, 0.0]])
+    sim = ref.similarity(a, e)
+    assert sim["cosine_min"] == pytest.approx(0.0, abs=1e-12)
+    assert sim["cosine_mean"] == pytest.approx(0.5)
+    assert sim["max_abs"] == pytest.approx(2.0)
+    same = ref.similarity(e, e)
+    assert same["cosine_min"] == pytest.approx(1.0) and same["relative_l2"] == 0.0
