@@ -357,8 +357,11 @@ def similarity(actual, expected) -> dict:
     a2 = a2.reshape(-1, a2.shape[-1]) if a2.ndim else a2.reshape(1, 1)
     e2 = e2.reshape(-1, e2.shape[-1]) if e2.ndim else e2.reshape(1, 1)
     dots = (a2 * e2).sum(-1)
-    norms = np.linalg.norm(a2, axis=-1) * np.linalg.norm(e2, axis=-1)
-    row_cos = dots / np.maximum(norms, 1e-300)
+    na_r, ne_r = np.linalg.norm(a2, axis=-1), np.linalg.norm(e2, axis=-1)
+    live = ne_r > 0   # rows that are exactly zero in the expected tensor have no direction
+    row_cos = dots[live] / np.maximum(na_r[live] * ne_r[live], 1e-300)
+    if row_cos.size == 0:
+        row_cos = np.ones(1)
     a, e = a2.reshape(-1), e2.reshape(-1)
     na, ne = np.linalg.norm(a), np.linalg.norm(e)
     cos = float(a @ e / (na * ne)) if na > 0 and ne > 0 else float("nan")
@@ -367,6 +370,7 @@ def similarity(actual, expected) -> dict:
         cosine=cos,
         cosine_min=float(row_cos.min()),
         cosine_mean=float(row_cos.mean()),
+        zero_rows_nonzero=int(np.count_nonzero(na_r[~live])),
         relative_l2=float(np.linalg.norm(diff) / max(ne, 1e-30)),
         max_abs=float(np.abs(diff).max()) if diff.size else 0.0,
     )

@@ -48,6 +48,7 @@ def _assert_dh(dh_gpu, dh_ref):
     """North-star dhidden bar: max error <= 2e-2 of max|dh| and cosine >= 0.9999,
     the cosine taken per row (compare.py:80-89 reports row cosines)."""
     sim = ref.similarity(dh_gpu, dh_ref)
+    assert sim["zero_rows_nonzero"] == 0, sim   # masked slots give exactly zero rows
     assert sim["cosine_min"] >= 0.9999, sim
     assert sim["max_abs"] <= 2e-2 * np.abs(dh_ref).max(), sim
 

@@ -305,3 +305,6 @@ def test_similarity_metrics():
     assert sim["max_abs"] == pytest.approx(2.0)
     same = ref.similarity(e, e)
     assert same["cosine_min"] == pytest.approx(1.0) and same["relative_l2"] == 0.0
+    z = np.array([[0.0, 0.0], [1.0, 1.0]])
+    assert ref.similarity(z, z)["cosine_min"] == pytest.approx(1.0)
+    assert ref.similarity(np.array([[1e-3, 0.0], [1.0, 1.0]]), z)["zero_rows_nonzero"] == 1
