@@ -67,6 +67,15 @@ struct RowTile {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint4*>(base + off[i]);
   }
+  __device__ __forceinline__ void load_one(uint4& v, const char* base, int i) const {
+    v = *reinterpret_cast<const uint4*>(base + off[i]);
+  }
+  // One row group of a stage with only `kvalid` valid K entries: chunks past the end
+  // read chunk 0 instead (in bounds) and are zeroed when stored (store_row with kvalid).
+  __device__ __forceinline__ void load_one_clamped(uint4& v, const char* base, int i, int kvalid) const {
+    const int c = (threadIdx.x & 7) * 8;
+    v = *reinterpret_cast<const uint4*>(base + off[i] - (c < kvalid ? 0u : (uint32_t)(c * 2)));
+  }
   // Stage with only `kvalid` (< BK) valid K entries: the rest reads chunk 0 and is zeroed.
   __device__ __forceinline__ void load_tail(uint4 (&v)[8], const char* base, int kvalid) const {
     const int c = (threadIdx.x & 7) * 8;
@@ -81,6 +90,14 @@ struct RowTile {
     }
   }
 };
+
+__device__ __forceinline__ void store_row(const uint4& v, lds_t* lds, int i, int kvalid = BK) {
+  const int tid = threadIdx.x;
+  const int row = i * 32 + (tid >> 3);
+  const uint32_t keep = (tid & 7) * 8 < kvalid ? 0xffffffffu : 0u;
+  const u32x4_t y = {v.x & keep, v.y & keep, v.z & keep, v.w & keep};
+  *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(lds + lds_off(row, tid & 7)) = y;
+}
 
 __device__ __forceinline__ void store_tile(const uint4 (&v)[8], lds_t* lds) {
   const int tid = threadIdx.x;
@@ -113,6 +130,13 @@ struct ColTile {
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[h][j] = *reinterpret_cast<const uint4*>(base + off[h] + j * ld_bytes);
   }
+  // K row j of group h with only `kvalid` valid K rows: rows past the end read the
+  // stage's first row instead (in bounds) and are zeroed when stored (store_col_t).
+  __device__ __forceinline__ void load_one_clamped(uint4& v, const char* base, int64_t ld_bytes, int h, int j,
+                                                   int kvalid) const {
+    const int rg = (threadIdx.x + h * kThreads) >> 5;
+    v = *reinterpret_cast<const uint4*>(base + (rg * 4 + j < kvalid ? off[h] + j * ld_bytes : 0));
+  }
   __device__ __forceinline__ void load_tail(uint4 (&v)[2][4], const char* base, int64_t ld_bytes, int kvalid) const {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -128,6 +152,28 @@ struct ColTile {
     }
   }
 };
+
+// Column c of group h of a transposed tile (see store_tile_t): one 8-byte LDS store.
+__device__ __forceinline__ void store_col_t(const uint4 (&v)[2][4], lds_t* lds, int h, int c, int kvalid) {
+  const int grp = threadIdx.x + h * kThreads;
+  const int rg = grp >> 5, cg = grp & 31;
+  // K rows 4 rg + j >= kvalid hold clamped re-reads: zero them
+  const uint32_t m01 = (rg * 4 + 0 < kvalid ? 0xffffu : 0u) | (rg * 4 + 1 < kvalid ? 0xffff0000u : 0u);
+  const uint32_t m23 = (rg * 4 + 2 < kvalid ? 0xffffu : 0u) | (rg * 4 + 3 < kvalid ? 0xffff0000u : 0u);
+  const uint32_t w0[4] = {v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w};
+  const uint32_t w1[4] = {v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w};
+  const uint32_t w2[4] = {v[h][2].x, v[h][2].y, v[h][2].z, v[h][2].w};
+  const uint32_t w3[4] = {v[h][3].x, v[h][3].y, v[h][3].z, v[h][3].w};
+  const int sh = (c & 1) * 16;
+  const uint32_t e0 = (w0[c >> 1] >> sh) & 0xffffu;
+  const uint32_t e1 = (w1[c >> 1] >> sh) & 0xffffu;
+  const uint32_t e2 = (w2[c >> 1] >> sh) & 0xffffu;
+  const uint32_t e3 = (w3[c >> 1] >> sh) & 0xffffu;
+  const int row = cg * 8 + c;
+  const int off = lds_off(row, rg >> 1) + (rg & 1) * 8;
+  const u32x2_t y = {(e0 | (e1 << 16)) & m01, (e2 | (e3 << 16)) & m23};
+  *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + off) = y;
+}
 
 __device__ __forceinline__ void store_tile_t(const uint4 (&v)[2][4], lds_t* lds) {
 #pragma unroll
@@ -158,45 +204,6 @@ struct Frags {
   bf16x8_t a[4], b[4];
 };
 
-__device__ __forceinline__ void load_frags(Frags& f, const lds_t* la, const lds_t* lb, int kk) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int r = lane & 31, kh = lane >> 5;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f.a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-        la + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
-    f.b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-        lb + lds_off(wn * 128 + i * 32 + r, kk * 2 + kh));
-  }
-}
-
-__device__ __forceinline__ void mma_frags(f32x16_t (&acc)[4][4], const Frags& f) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
-}
-
-// One BK stage (four 16-wide K steps): fragments of step k+1 load while the 16 MFMAs
-// of step k run; `mid` (the next stage's LDS stores and global prefetch) is issued
-// after the second step so that it overlaps the remaining MFMAs.
-template <typename Mid>
-__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la, const lds_t* lb, Mid&& mid) {
-  Frags f0, f1;
-  load_frags(f0, la, lb, 0);
-  load_frags(f1, la, lb, 1);
-  mma_frags(acc, f0);
-  load_frags(f0, la, lb, 2);
-  mma_frags(acc, f1);
-  mid();
-  load_frags(f1, la, lb, 3);
-  mma_frags(acc, f0);
-  mma_frags(acc, f1);
-}
-
 __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[4][4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -206,8 +213,59 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[4][4]) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 }
 
+// Operand rows i of fragment step kk (one A and one B fragment).
+__device__ __forceinline__ void load_frag_pair(Frags& f, const lds_t* la, const lds_t* lb, int kk, int i) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 31, kh = lane >> 5;
+  f.a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+      la + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
+  f.b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+      lb + lds_off(wn * 128 + i * 32 + r, kk * 2 + kh));
+}
+
+// [begin, end) of the memory operations issued after MFMA group q (of 4) when a step
+// carries n of them: 1/8, 1/8, 3/8, 3/8 of n, so the early groups leave room for the
+// next step's fragment reads.
+__device__ __forceinline__ constexpr int quarter_begin(int q, int n) {
+  return q == 0 ? 0 : q == 1 ? n / 8 : q == 2 ? n / 4 : q == 3 ? (n * 5) / 8 : n;
+}
+
+// One BK stage: 64 MFMAs in 16 groups of 4.  With one wave per SIMD the matrix core is
+// busy only while its wave issues MFMAs, and a burst of 16-byte global loads or LDS
+// stores stalls in-order issue; so after each MFMA group the wave issues a few of the
+// stage's other instructions: the next step's fragment reads (groups 0-1) and
+// mem(kk, q) -- the next stage's LDS stores (steps 0-1) and the prefetch of the stage
+// after it (steps 2-3).  sched_barrier keeps the compiler from regrouping them.
+template <typename Mem>
+__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la, const lds_t* lb, Mem&& mem) {
+  Frags f[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) load_frag_pair(f[0], la, lb, 0, i);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int cb = kk & 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[cb].a[q], f[cb].b[j], acc[q][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk < 3 && q < 2) {
+        load_frag_pair(f[cb ^ 1], la, lb, kk + 1, 2 * q);
+        load_frag_pair(f[cb ^ 1], la, lb, kk + 1, 2 * q + 1);
+      }
+      mem(kk, q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 // acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T, both row-major with K contiguous and
-// K a multiple of BK.  Ends with a barrier (LDS free for the caller).
+// K a multiple of BK.  Ends with a barrier (LDS free for the caller).  The prefetch
+// past the last stage re-reads the last stage (clamped) and its LDS stores land in
+// the idle buffer, so every stage runs the same straight-line body.
 __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
                                         int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
                                         int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
@@ -217,27 +275,31 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
   tb.init(ldb, b0, bmax);
   const char* pa = reinterpret_cast<const char*>(A + a0 * lda);
   const char* pb = reinterpret_cast<const char*>(B + b0 * ldb);
+  const int64_t last = (int64_t)(KT - 1) * BK * 2;
   uint4 ra[8], rb[8];
   ta.load(ra, pa);
   tb.load(rb, pb);
   store_tile(ra, lds);
   store_tile(rb, lds + kStageBytes);
   __syncthreads();
-  if (KT > 1) {
-    ta.load(ra, pa + BK * 2);
-    tb.load(rb, pb + BK * 2);
+  {
+    const int64_t k1 = BK * 2 < last ? BK * 2 : last;
+    ta.load(ra, pa + k1);
+    tb.load(rb, pb + k1);
   }
   for (int kt = 0; kt < KT; ++kt) {
-    lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
+    const lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
     lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
-    mma_stage(acc, cur, cur + kStageBytes, [&]() {
-      if (kt + 1 < KT) {
-        store_tile(ra, nxt);
-        store_tile(rb, nxt + kStageBytes);
-      }
-      if (kt + 2 < KT) {
-        ta.load(ra, pa + (int64_t)(kt + 2) * BK * 2);
-        tb.load(rb, pb + (int64_t)(kt + 2) * BK * 2);
+    int64_t kp = (int64_t)(kt + 2) * BK * 2;
+    kp = kp < last ? kp : last;
+    mma_stage(acc, cur, cur + kStageBytes, [&](int kk, int q) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i < quarter_begin(q, 8) || i >= quarter_begin(q + 1, 8)) continue;
+        if (kk == 0) store_row(ra[i], nxt, i);
+        if (kk == 1) store_row(rb[i], nxt + kStageBytes, i);
+        if (kk == 2) ta.load_one(ra[i], pa + kp, i);
+        if (kk == 3) tb.load_one(rb[i], pb + kp, i);
       }
     });
     __syncthreads();
@@ -246,7 +308,7 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
 
 // acc += A[a0:a0+256, k0:k1] . B[k0:k1, c0:c0+256] with A row-major (K contiguous) and
 // B row-major [K, cols] (columns contiguous, transposed through LDS).  Entries with
-// K >= kmax are zero.  Ends with a barrier.
+// K >= kmax are zero.  Ends with a barrier.  Same stage structure as gemm_nt.
 __device__ __forceinline__ void gemm_nn(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
                                         int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
                                         int64_t c0, int64_t cmax, int64_t k0, int64_t k1, int64_t kmax,
@@ -261,33 +323,53 @@ __device__ __forceinline__ void gemm_nn(f32x16_t (&acc)[4][4], const uint16_t* _
   const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
   const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
   uint4 ra[8], rb[2][4];
-  auto load_stage = [&](int kt) {
+  // stage bases and valid K count; stages past the end re-read the last one
+  auto stage_of = [&](int kt, const char*& a, const char*& b, int& kv) {
+    kt = kt < KT - 1 ? kt : KT - 1;
     const int64_t kvalid = kmax - (k0 + (int64_t)kt * BK);
-    const char* a = pa + (int64_t)kt * BK * 2;
-    const char* b = pb + (int64_t)kt * BK * ldb_bytes;
-    if (kvalid >= BK) {
-      ta.load(ra, a);
-      tb.load(rb, b, ldb_bytes);
-    } else {
-      ta.load_tail(ra, a, (int)kvalid);
-      tb.load_tail(rb, b, ldb_bytes, (int)kvalid);
-    }
+    kv = kvalid < BK ? (int)kvalid : BK;
+    a = pa + (int64_t)kt * BK * 2;
+    b = pb + (int64_t)kt * BK * ldb_bytes;
   };
-  load_stage(0);
-  store_tile(ra, lds);
-  store_tile_t(rb, lds + kStageBytes);
-  __syncthreads();
-  if (KT > 1) load_stage(1);
+  int kv1;
+  {
+    const char *a, *b;
+    int kv;
+    stage_of(0, a, b, kv);
+    ta.load_tail(ra, a, kv);
+    tb.load_tail(rb, b, ldb_bytes, kv);
+    store_tile(ra, lds);
+    store_tile_t(rb, lds + kStageBytes);
+    __syncthreads();
+    stage_of(1, a, b, kv1);
+    ta.load_tail(ra, a, kv1);
+    tb.load_tail(rb, b, ldb_bytes, kv1);
+  }
+  int ckv = kv1;  // valid K entries of the stage held in registers
   for (int kt = 0; kt < KT; ++kt) {
-    lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
+    const lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
     lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
-    mma_stage(acc, cur, cur + kStageBytes, [&]() {
-      if (kt + 1 < KT) {
-        store_tile(ra, nxt);
-        store_tile_t(rb, nxt + kStageBytes);
+    const char *na, *nb;
+    int nkv;
+    stage_of(kt + 2, na, nb, nkv);
+    mma_stage(acc, cur, cur + kStageBytes, [&](int kk, int q) {
+      if (kk == 1) {
+#pragma unroll
+        for (int idx = 0; idx < 16; ++idx) {
+          if (idx < quarter_begin(q, 16) || idx >= quarter_begin(q + 1, 16)) continue;
+          store_col_t(rb, nxt + kStageBytes, idx >> 3, idx & 7, ckv);
+        }
+        return;
       }
-      if (kt + 2 < KT) load_stage(kt + 2);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i < quarter_begin(q, 8) || i >= quarter_begin(q + 1, 8)) continue;
+        if (kk == 0) store_row(ra[i], nxt, i, ckv);
+        if (kk == 2) ta.load_one_clamped(ra[i], na, i, nkv);
+        if (kk == 3) tb.load_one_clamped(rb[i >> 2][i & 3], nb, ldb_bytes, i >> 2, i & 3, nkv);
+      }
     });
+    ckv = nkv;
     __syncthreads();
   }
 }
