@@ -38,9 +38,14 @@ int check_slots(const int64_t* labels, const float* weights, const uint8_t* vali
   return NS_OK;
 }
 
+constexpr int64_t kMaxLd = int64_t(1) << 23;
+
 int check_matrix(const void* p, int64_t n, int64_t cols, int64_t ld, const char* name) {
   if (n > 0 && cols > 0 && !p) return fail(NS_ENULL, "%s is NULL", name);
   if (ld < cols) return fail(NS_EINVAL, "%s: leading dimension %lld < columns %lld", name, (long long)ld, (long long)cols);
+  // kernels address a 256-row tile with 32-bit byte offsets: 256 * ld * 2 bytes < 2^32
+  if (ld > kMaxLd)
+    return fail(NS_EINVAL, "%s: leading dimension %lld exceeds %lld elements", name, (long long)ld, (long long)kMaxLd);
   return NS_OK;
 }
 

@@ -262,48 +262,123 @@ __device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la
   }
 }
 
+// One 256-row operand tile fetched straight into LDS (global_load_lds_dwordx4): wave wv
+// issues 8 instructions per stage, instruction i filling the 1 KB LDS block wv * 8 + i,
+// i.e. rows 8 (wv * 8 + i) .. +8.  Lane l writes the block's 16-byte slot l, which is
+// physical chunk l % 8 of row 8 (wv * 8 + i) + l / 8; the lane therefore fetches the
+// logical chunk (l % 8) ^ swz(row), so the tile lands in the swizzled lds_off layout.
+// Rows past rmax re-read row rmax - 1 (their results are discarded by the caller).
+struct DmaTile {
+  uint32_t off[8];  // per-lane byte offsets from the tile's first row, stage 0
+  __device__ __forceinline__ void init(int64_t ld, int64_t r0, int64_t rmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = (wv * 8 + i) * 8 + (lane >> 3);
+      int64_t r = r0 + row;
+      r = r < rmax ? r : rmax - 1;
+      const int chunk = (lane & 7) ^ swz(row);
+      off[i] = (uint32_t)(((r - r0) * ld + chunk * 8) * 2);
+    }
+  }
+  // instruction i of one stage: `base` = the tile's first row at this stage's K offset,
+  // `dst` = the operand's LDS stage buffer (wave-uniform)
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
+                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * 8 + i) * 1024),
+                                     16, 0, 0);
+  }
+};
+
+// Wait for this wave's LDS fills and all outstanding memory operations, then a
+// workgroup barrier.  The empty asm statements keep the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void fill_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T, both row-major with K contiguous and
-// K a multiple of BK.  Ends with a barrier (LDS free for the caller).  The prefetch
-// past the last stage re-reads the last stage (clamped) and its LDS stores land in
-// the idle buffer, so every stage runs the same straight-line body.
+// K a multiple of BK.  Ends with a barrier (LDS free for the caller).
+//
+// Operands go global -> LDS without registers; stage t lives in LDS buffer t & 1.  A
+// stage's 64 MFMAs run one per instruction slot with the other work of the stage
+// between them:
+//   step 0: fragment reads for step 1 | B fills of stage t + 1
+//   steps 1, 2: fragment reads for the next step
+//   step 3: after four groups, fill_barrier (stage t + 1 complete, buffer t & 1 read by
+//           everyone), then fragment reads of stage t + 1 step 0 and the A fills of
+//           stage t + 2 into buffer t & 1.
+// Fills past the last stage re-read the last stage into the idle buffer.
 __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
                                         int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
                                         int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
   const int KT = (int)(K / BK);
-  RowTile ta, tb;
-  ta.init(lda, a0, amax);
-  tb.init(ldb, b0, bmax);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  DmaTile ta, tb;
+  ta.init(lda, a0, amax, wv);
+  tb.init(ldb, b0, bmax, wv);
   const char* pa = reinterpret_cast<const char*>(A + a0 * lda);
   const char* pb = reinterpret_cast<const char*>(B + b0 * ldb);
-  const int64_t last = (int64_t)(KT - 1) * BK * 2;
-  uint4 ra[8], rb[8];
-  ta.load(ra, pa);
-  tb.load(rb, pb);
-  store_tile(ra, lds);
-  store_tile(rb, lds + kStageBytes);
-  __syncthreads();
-  {
-    const int64_t k1 = BK * 2 < last ? BK * 2 : last;
-    ta.load(ra, pa + k1);
-    tb.load(rb, pb + k1);
-  }
-  for (int kt = 0; kt < KT; ++kt) {
-    const lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
-    lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
-    int64_t kp = (int64_t)(kt + 2) * BK * 2;
-    kp = kp < last ? kp : last;
-    mma_stage(acc, cur, cur + kStageBytes, [&](int kk, int q) {
+  auto stage_k = [&](int t) -> int64_t { return (int64_t)(t < KT - 1 ? t : KT - 1) * BK * 2; };
+  auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * 2 * kStageBytes; };
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i < quarter_begin(q, 8) || i >= quarter_begin(q + 1, 8)) continue;
-        if (kk == 0) store_row(ra[i], nxt, i);
-        if (kk == 1) store_row(rb[i], nxt + kStageBytes, i);
-        if (kk == 2) ta.load_one(ra[i], pa + kp, i);
-        if (kk == 3) tb.load_one(rb[i], pb + kp, i);
-      }
-    });
-    __syncthreads();
+  for (int i = 0; i < 8; ++i) ta.issue(pa, buf(0), wv, i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tb.issue(pb, buf(0) + kStageBytes, wv, i);
+  fill_barrier();
+  Frags f[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) load_frag_pair(f[0], buf(0), buf(0) + kStageBytes, 0, i);
+  {
+    const int64_t k1 = stage_k(1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ta.issue(pa + k1, buf(1), wv, i);
   }
+  for (int t = 0; t < KT; ++t) {
+    const lds_t* cur = buf(t);
+    lds_t* nxt = buf(t + 1);
+    const int64_t k1 = stage_k(t + 1), k2 = stage_k(t + 2);
+    const int lane = threadIdx.x & 63;
+    const int wm = wv >> 1, wn = wv & 1;
+    const int r = lane & 31, kh = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int cb = kk & 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[cb].a[q], f[cb].b[j], acc[q][j], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          const int i = 2 * (q & 1) + (j >> 1);
+          if (kk < 3 && q < 2) {
+            if ((j & 1) == 0)
+              f[cb ^ 1].a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                  cur + lds_off(wm * 128 + i * 32 + r, (kk + 1) * 2 + kh));
+            else
+              f[cb ^ 1].b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                  cur + kStageBytes + lds_off(wn * 128 + i * 32 + r, (kk + 1) * 2 + kh));
+          }
+          if (kk == 0 && q >= 2) tb.issue(pb + k1, nxt + kStageBytes, wv, (q - 2) * 4 + j);
+          if (kk == 3 && q >= 2) {
+            if ((j & 1) == 0)
+              f[0].a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                  nxt + lds_off(wm * 128 + i * 32 + r, kh));
+            else
+              f[0].b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                  nxt + kStageBytes + lds_off(wn * 128 + i * 32 + r, kh));
+            ta.issue(pa + k2, buf(t), wv, (q - 2) * 4 + j);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (kk == 3 && q == 1) fill_barrier();
+      }
+    }
+  }
+  fill_barrier();
 }
 
 // acc += A[a0:a0+256, k0:k1] . B[k0:k1, c0:c0+256] with A row-major (K contiguous) and

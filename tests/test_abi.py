@@ -50,6 +50,7 @@ def _fwd(lib, **over):
     (dict(n=12), -1, "multiple of the block size"),
     (dict(k=0), -1, "block size"),
     (dict(ldz=8), -1, "leading dimension"),
+    (dict(ldu=(1 << 23) + 1), -1, "exceeds"),     # tiles use 32-bit byte offsets
     (dict(z=None), -5, "z is NULL"),
     (dict(labels=None), -5, "non-NULL"),
     (dict(wsb=16), -4, "workspace"),
