@@ -381,6 +381,150 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
   fill_barrier();
 }
 
+// B operand [K rows, cols] (cols contiguous) fetched straight into a row-major LDS
+// stage: 64 K rows of 512 bytes, the 16-byte chunk cn of row k stored at physical
+// chunk cn ^ (4 (k & 3)), which keeps the transposed fragment reads (tr_b16) free of
+// bank conflicts.  Instruction i of wave wv fills rows 2 (wv * 8 + i) + {0, 1}; lane l
+// writes physical chunk l % 32 of row 2 (wv * 8 + i) + l / 32.  Column chunks at or
+// past cmax re-read the tile's first chunk (discarded by the caller).
+struct DmaTileKN {
+  uint32_t off[8];
+  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 2 * (wv * 8 + i) + (lane >> 5);
+      const int cn = (lane & 31) ^ (4 * (row & 3));
+      int64_t col = c0 + cn * 8;
+      col = col < cmax ? col : c0;
+      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
+                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * 8 + i) * 1024),
+                                     16, 0, 0);
+  }
+};
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// B fragment i (32 columns) of step kk from a DmaTileKN stage, as two transposed reads:
+// ds_read_b64_tr_b16 gives lane 16 g + x of a 16-lane group element x % 4 of the
+// 8-byte pieces addressed by lanes 16 g + 4 j + x / 4, j = 0..3.  Lane 16 g + 4 j + m
+// addresses row kbase + j, columns nb + 4 m .. +3, so lane 16 g + x receives
+// B[kbase + 0..3][nb + x]: K-contiguous, as the MFMA B operand wants.
+struct TrFrag {
+  i16x4_t lo, hi;  // K 0..3 and 4..7 of this lane's eight
+};
+
+__device__ __forceinline__ uint32_t tr_base(int wn, int i) {
+  // byte address of this lane's piece for step 0, half 0 (add 2048 for half 1, 8192 per step)
+  const int lane = threadIdx.x & 63;
+  const int x = lane & 15;
+  const int row = 8 * (lane >> 5) + (x >> 2);                       // + 16 kk + 4 half
+  const int col = wn * 128 + i * 32 + 16 * ((lane >> 4) & 1) + 4 * (x & 3);
+  const int cn = (col >> 3) ^ (4 * (row & 3));
+  return (uint32_t)(row * 512 + (cn << 4) + (col & 7) * 2);
+}
+
+__device__ __forceinline__ i16x4_t tr_read(const lds_t* buf, uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) i16x4_t*>(const_cast<lds_t*>(buf) + addr));
+}
+
+__device__ __forceinline__ bf16x8_t tr_join(const TrFrag& f) {
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(f.lo, f.hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// acc += A[a0:a0+256, k0:k0+64 KT] . B[k0:k0+64 KT, c0:c0+256] over KT full stages,
+// A row-major (K contiguous), B row-major [K, cols].  Both operands go global -> LDS
+// without registers, as in gemm_nt; B fragments use transposed LDS reads.  Per stage t:
+//   steps 0-2: the next step's 12 fragment reads (4 A, 8 B halves), one per MFMA;
+//   step 0: the B fills of stage t + 1 in the first eight MFMA slots;
+//   step 3: fill_barrier after two groups, then stage t + 1's step-0 fragments and the
+//           A fills of stage t + 2.
+// Ends with a barrier.  KT >= 1.
+__device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
+                                            int64_t a0, int64_t amax, const uint16_t* __restrict__ B,
+                                            int64_t ldb, int64_t c0, int64_t cmax, int64_t k0, int KT,
+                                            lds_t* lds) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  DmaTile ta;
+  DmaTileKN tb;
+  ta.init(lda, a0, amax, wv);
+  tb.init(ldb, c0, cmax, wv);
+  const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
+  const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
+  const int64_t ldb_stage = (int64_t)BK * ldb * 2;
+  auto clampt = [&](int t) -> int64_t { return (int64_t)(t < KT - 1 ? t : KT - 1); };
+  auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * 2 * kStageBytes; };
+  const int lane = threadIdx.x & 63;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int r = lane & 31, kh = lane >> 5;
+  uint32_t tb_addr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tb_addr[i] = tr_base(wn, i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ta.issue(pa, buf(0), wv, i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tb.issue(pb, buf(0) + kStageBytes, wv, i);
+  fill_barrier();
+  bf16x8_t fa[2][4];
+  TrFrag fb[2][4];
+  // read op o (0..11) of step kk from stage buffer `sb` into set `c`: A i, B i lo, B i hi
+  auto read_op = [&](int c, const lds_t* sb, int kk, int o) {
+    const int i = o / 3, part = o % 3;
+    if (part == 0)
+      fa[c][i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+          sb + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
+    else if (part == 1)
+      fb[c][i].lo = tr_read(sb + kStageBytes, tb_addr[i] + kk * 8192);
+    else
+      fb[c][i].hi = tr_read(sb + kStageBytes, tb_addr[i] + kk * 8192 + 2048);
+  };
+#pragma unroll
+  for (int o = 0; o < 12; ++o) read_op(0, buf(0), 0, o);
+  {
+    const int64_t t1 = clampt(1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ta.issue(pa + t1 * BK * 2, buf(1), wv, i);
+  }
+  for (int t = 0; t < KT; ++t) {
+    const lds_t* cur = buf(t);
+    lds_t* nxt = buf(t + 1);
+    const int64_t t1 = clampt(t + 1), t2 = clampt(t + 2);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int cb = kk & 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int sl = q * 4 + j;
+          acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][q], tr_join(fb[cb][j]), acc[q][j], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          if (kk < 3 && sl < 12) read_op(cb ^ 1, cur, kk + 1, sl);
+          if (kk == 0 && sl < 8) tb.issue(pb + t1 * ldb_stage, nxt + kStageBytes, wv, sl);
+          if (kk == 3 && sl >= 8) {
+            const int u = sl - 8;
+            if (u < 4) {
+              read_op(0, nxt, 0, 2 * u);
+              read_op(0, nxt, 0, 2 * u + 1);
+            } else {
+              read_op(0, nxt, 0, 4 + u);
+            }
+            ta.issue(pa + t2 * BK * 2, buf(t), wv, u);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (kk == 3 && q == 1) fill_barrier();
+      }
+    }
+  }
+  fill_barrier();
+}
+
 // acc += A[a0:a0+256, k0:k1] . B[k0:k1, c0:c0+256] with A row-major (K contiguous) and
 // B row-major [K, cols] (columns contiguous, transposed through LDS).  Entries with
 // K >= kmax are zero.  Ends with a barrier.  Same stage structure as gemm_nt.
@@ -698,7 +842,15 @@ void dh_kernel(BwdParams p) {
   const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)ct * BN;
   f32x16_t acc[4][4];
   zero_acc(acc);
-  gemm_nn(acc, p.dl, p.ldd, m0, p.n, p.weight, p.ldw, c0, p.d, (int64_t)kt0 * BK, (int64_t)kt1 * BK, p.v, lds);
+  // full stages straight into LDS; a partial last stage (V % BK != 0) through registers,
+  // where entries past V are zeroed
+  const int kfull = (int)(p.v / BK);
+  const int kt_dma_end = kt1 < kfull ? kt1 : kfull;
+  if (kt_dma_end > kt0)
+    gemm_nn_dma(acc, p.dl, p.ldd, m0, p.n, p.weight, p.ldw, c0, p.d, (int64_t)kt0 * BK, kt_dma_end - kt0, lds);
+  if (kt1 > kt_dma_end)
+    gemm_nn(acc, p.dl, p.ldd, m0, p.n, p.weight, p.ldw, c0, p.d, (int64_t)kt_dma_end * BK, (int64_t)kt1 * BK, p.v,
+            lds);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int h = lane >> 5;
