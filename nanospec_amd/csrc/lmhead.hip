@@ -613,9 +613,20 @@ __device__ __forceinline__ void dump_half(const f32x16_t (&acc)[4][4], lds_t* ld
 }
 
 // Workgroup -> (token tile, vocab split) map.  Workgroups are dispatched round-robin over
-// the 8 XCDs; logical ids are laid out so that each XCD holds consecutive ids, and
-// consecutive ids share a vocab split (the W stream) across token tiles.
-__device__ __forceinline__ void wg_coords(int g, int G, int TT, int& t, int& s) {
+// the 8 XCDs, and the C = G / 8 workgroups of one XCD share its L2.  With xa > 0 each
+// XCD holds a block of xa token tiles x (C / xa) vocab splits, so one K stage of the
+// block reads xa + C / xa distinct operand tiles through that L2 (12 for a 4 x 8 block,
+// against 18 for 16 token tiles x 2 splits).  xa = 0: consecutive ids per XCD, token
+// tile fastest.
+__device__ __forceinline__ void wg_coords(int g, int G, int TT, int xa, int& t, int& s) {
+  if (xa > 0) {
+    const int C = G / kNumXcd, xb = C / xa;
+    const int x = g % kNumXcd, r = g / kNumXcd;
+    const int groups_t = TT / xa;
+    t = (x % groups_t) * xa + r % xa;
+    s = (x / groups_t) * xb + r / xa;
+    return;
+  }
   int L = g;
   if (G % kNumXcd == 0) L = (g % kNumXcd) * (G / kNumXcd) + g / kNumXcd;
   s = L / TT;
@@ -632,6 +643,7 @@ struct HeadParams {
   int64_t ldh, ldw, ldm, ldt;
   int64_t n, d, v;
   int tt, vt, splits;       // token tiles, vocab tiles, vocab splits
+  int xa;                   // token tiles per XCD block (wg_coords), 0 = unblocked
   const int64_t* labels;
   const float* weights;
   float c_ce, c_kl, inv_acc;
@@ -733,7 +745,7 @@ void head_kernel(HeadParams p) {
   lds_t* lds = (lds_t*)lds_raw;
   lds_f32* zt = reinterpret_cast<lds_f32*>(lds);
   int tile_t, split;
-  wg_coords(blockIdx.x, gridDim.x, p.tt, tile_t, split);
+  wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, tile_t, split);
   const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
   const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
   const int tid = threadIdx.x;
@@ -820,6 +832,7 @@ struct BwdParams {
   int64_t ldd, ldw;
   int64_t n, v, d;
   int mt, ct, ksplit;      // token tiles, d tiles, K splits
+  int xa, xb;              // XCD block: xa token tiles x xb d tiles per round (0 = unblocked)
   int kt_total;            // ceil(V / BK)
   float* part;             // [ksplit][N][d] fp32
 };
@@ -828,15 +841,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 void dh_kernel(BwdParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_t* lds = (lds_t*)lds_raw;
-  // Tile order: consecutive workgroups share a K split and a d tile (W stream) across
-  // token tiles; XCD-aware like the forward.
+  // Tile order.  Workgroups go round-robin to the 8 XCDs and run in rounds of
+  // C = xa * xb per XCD (one per CU).  With xa > 0 each round of one XCD is a block of
+  // xa token tiles x xb d tiles of one K split, so a K stage reads xa + xb distinct
+  // operand tiles through that XCD's L2; blocks are numbered token group fastest, then
+  // d group, then K split.  xa = 0: consecutive ids per XCD, token tile fastest.
   const int G = gridDim.x;
-  int L = blockIdx.x;
-  if (G % kNumXcd == 0) L = (L % kNumXcd) * (G / kNumXcd) + L / kNumXcd;
-  const int mt = L % p.mt;
-  const int rest = L / p.mt;
-  const int ct = rest % p.ct;
-  const int ks = rest / p.ct;
+  const int g = blockIdx.x;
+  int mt, ct, ks;
+  if (p.xa > 0) {
+    const int C = p.xa * p.xb;
+    const int i = g / kNumXcd;
+    const int blk = (i / C) * kNumXcd + g % kNumXcd, r = i % C;
+    const int gm = p.mt / p.xa, gc = p.ct / p.xb;
+    mt = (blk % gm) * p.xa + r % p.xa;
+    ct = ((blk / gm) % gc) * p.xb + r / p.xa;
+    ks = blk / (gm * gc);
+  } else {
+    int L = g;
+    if (G % kNumXcd == 0) L = (L % kNumXcd) * (G / kNumXcd) + L / kNumXcd;
+    mt = L % p.mt;
+    const int rest = L / p.mt;
+    ct = rest % p.ct;
+    ks = rest / p.ct;
+  }
   const int kt0 = (int)((int64_t)ks * p.kt_total / p.ksplit);
   const int kt1 = (int)((int64_t)(ks + 1) * p.kt_total / p.ksplit);
   const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)ct * BN;
@@ -898,7 +926,23 @@ int device_cus() {
 
 struct HeadPlan {
   int tt, vt, splits, grid;
+  int xa;  // token tiles per XCD block, 0 = unblocked (wg_coords)
 };
+
+// Token tiles per XCD block for a tt x splits grid: a divisor a of C = grid / 8 with
+// tt % a == 0 and splits % (C / a) == 0, minimising a + C / a (distinct operand tiles
+// per K stage in one L2); 0 when no such block exists.
+int xcd_block(int tt, int splits) {
+  const int grid = tt * splits;
+  if (grid % kNumXcd) return 0;
+  const int C = grid / kNumXcd;
+  int best = 0;
+  for (int a = 1; a <= C; ++a) {
+    if (C % a || tt % a || splits % (C / a)) continue;
+    if (best == 0 || a + C / a < best + C / best) best = a;
+  }
+  return best;
+}
 
 HeadPlan head_plan(int64_t n, int64_t v) {
   HeadPlan pl;
@@ -910,6 +954,7 @@ HeadPlan head_plan(int64_t n, int64_t v) {
   if (s > pl.vt) s = pl.vt;
   pl.splits = s;
   pl.grid = pl.tt * s;
+  pl.xa = xcd_block(pl.tt, s);
   return pl;
 }
 
@@ -935,6 +980,7 @@ size_t head_ws_layout(int64_t n, int64_t v, void* base, HeadWs* out) {
 
 struct BwdPlan {
   int mt, ct, ksplit, kt_total, grid;
+  int xa, xb;  // XCD block (dh_kernel's tile order), 0 = unblocked
 };
 
 BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d) {
@@ -950,6 +996,17 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d) {
   if (ks > pl.kt_total) ks = pl.kt_total;
   pl.ksplit = ks;
   pl.grid = tiles * ks;
+  // XCD block (dh_kernel's tile order): xa * xb = CUs per XCD, xa | mt, xb | ct, whole
+  // rounds on every XCD; the smallest xa + xb
+  pl.xa = pl.xb = 0;
+  if (cus % kNumXcd == 0) {
+    const int C = cus / kNumXcd;
+    for (int a = 1; a <= C; ++a) {
+      const int b = C / a;
+      if (C % a || pl.mt % a || pl.ct % b || pl.grid % (kNumXcd * C)) continue;
+      if (pl.xa == 0 || a + b < pl.xa + pl.xb) { pl.xa = a; pl.xb = b; }
+    }
+  }
   return pl;
 }
 
@@ -1000,7 +1057,7 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
   p.teacher = teacher;
   p.ldh = ldh; p.ldw = ldw; p.ldm = ldm; p.ldt = ldt;
   p.n = a.n; p.d = d; p.v = v;
-  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits;
+  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa;
   p.labels = a.labels; p.weights = a.weights;
   p.c_ce = a.c_ce; p.c_kl = a.c_kl; p.inv_acc = a.inv_acc;
   p.part1 = w.part1; p.zy = w.zy; p.parta = w.parta;
@@ -1023,6 +1080,7 @@ hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int6
   p.weight = static_cast<const uint16_t*>(weight);
   p.ldd = ldd; p.ldw = ldw; p.n = n; p.v = v; p.d = d;
   p.mt = pl.mt; p.ct = pl.ct; p.ksplit = pl.ksplit; p.kt_total = pl.kt_total;
+  p.xa = pl.xa; p.xb = pl.xb;
   p.part = static_cast<float*>(ws);
   static bool attr_set = false;
   if (!attr_set) {
@@ -1054,7 +1112,7 @@ hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t
   p.markov = static_cast<const uint16_t*>(addend);
   p.ldh = ldx; p.ldw = ldw; p.ldm = lda;
   p.n = n; p.d = d; p.v = v;
-  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits;
+  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa;
   p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
   p.teacher = nullptr;
   return launch_head<MODE_STORE, uint16_t>(p, pl.grid, st, "head_linear");

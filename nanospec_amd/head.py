@@ -115,13 +115,13 @@ def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, retu
     """dh = dl . W_lm with the dl emitted by the forward.  Returns dh [..., d] bf16
     (and dl [..., V] bf16 when ``return_dlogits``, for the Markov backward)."""
     if saved.dlogits is None:
-        raise ValueError("the forward ran with emit_dlogits=False; no dl to propagate")
+        raise ValueError("no dl to propagate: the forward ran with emit_dlogits=False, or the backward already ran")
     if accumulation_steps != saved.accumulation_steps:
         raise ValueError(
             f"dl was emitted for accumulation_steps={saved.accumulation_steps}; pass the same value "
             "to lm_head_ce_kl_loss and lm_head_ce_kl_backward"
         )
-    dl = saved.dlogits
+    dl, saved.dlogits = saved.dlogits, None   # handed over once, so it is freed after dh unless returned
     dh = lm_head_linear_backward(dl, saved.weight)
     dl = dl.view(saved.shape)
     dh = dh.view(saved.shape[:-1] + (saved.weight.shape[1],))
