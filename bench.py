@@ -36,6 +36,12 @@ def parse():
     p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU-baseline sample (0: default)")
+    p.add_argument("--pmc-driver", action="store_true",
+                   help="short run for one rocprofv3 --pmc pass: a 1 GiB calibration kernel, then two steps")
+    p.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="print the HBM-traffic summary of two --pmc-driver passes (FETCH_SIZE, WRITE_SIZE)")
+    p.add_argument("--stats-from", metavar="DIR", help="print a summary of a rocprofv3 --stats csv run")
+    p.add_argument("--command", default="", help="command line recorded in a printed summary")
     return p.parse_args()
 
 
@@ -48,6 +54,136 @@ def cpu_model() -> str:
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+# --------------------------------------------------------------------------- profiles
+
+# library kernel symbol (demangled, as rocprofv3 prints it) -> the launch-site name the
+# library's own timer (ns_profile_*) uses
+KERNEL_NAMES = [
+    (r"head_kernel<0,", "head_stats"),
+    (r"head_kernel<1,", "head_emit"),
+    (r"head_kernel<2,", "head_linear"),
+    (r"dh_reduce_kernel", "dh_reduce"),
+    (r"dh_kernel", "dh_gemm"),
+    (r"stream_stats_kernel", "stream_stats"),
+    # stream_emit_kernel<TZ, TU, TD, VEC, EMIT, ACCEPT>
+    (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), true", "stream_emit"),
+    (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), false", "stream_accept"),
+    (r"merge_kernel", "merge_rows"),
+    (r"finalize_kernel", "finalize_metrics"),
+    (r"fp8_quant_kernel", "fp8_quant"),
+    (r"fp8_head_kernel", "fp8_head_gemm"),
+    (r"prepare_kernel", "prepare_slots"),
+]
+# profiles/<prefix>_traffic.md and <prefix>_kernel_stats.md: named for the kernels and workload
+PROFILE_PREFIX = {"c1": "stream_c1", "c2": "lmhead_c2", "c3": "lmhead_c3", "c4": "fp8_lmhead_c4"}
+CALIBRATION_BYTES = 1 << 30   # the --pmc-driver calibration (fp32 negation): reads and writes 1 GiB
+
+
+def timer_name(kernel: str):
+    import re
+
+    if "ns::" not in kernel:
+        return None
+    for pat, name in KERNEL_NAMES:
+        if re.search(pat, kernel):
+            return name
+    return None
+
+
+def _csv_rows(directory: str, suffix: str):
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _counter_per_kernel(directory: str, counter: str):
+    """Median per-dispatch value (KiB) of `counter` for each library kernel, plus the
+    calibration kernel's value."""
+    import statistics
+
+    per, calib = {}, []
+    rows = [r for r in _csv_rows(directory, "counter_collection.csv") if r["Counter_Name"] == counter]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    seen_library = False   # the calibration kernel follows the driver's first step
+    for r in rows:
+        val = float(r["Counter_Value"])
+        name = timer_name(r["Kernel_Name"])
+        if name:
+            seen_library = True
+            per.setdefault(name, []).append(val)
+        elif seen_library and "neg" in r["Kernel_Name"]:
+            calib.append(val)
+    if not calib:
+        raise SystemExit(f"no calibration dispatch (torch.neg) in {directory}")
+    return {k: statistics.median(v) for k, v in per.items()}, max(calib)
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, config: str, command: str) -> str:
+    """Markdown: per-kernel HBM bytes per launch from FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled so that the calibration kernel reads (writes) exactly 1 GiB."""
+    fetch, fcal = _counter_per_kernel(fetch_dir, "FETCH_SIZE")
+    write, wcal = _counter_per_kernel(write_dir, "WRITE_SIZE")
+    ff = CALIBRATION_BYTES / (fcal * 1024.0)
+    wf = CALIBRATION_BYTES / (wcal * 1024.0)
+    out = [f"# HBM traffic per launch: {config.upper()} kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
+           "Commands (from the repository root on the MI355X box):", "", "```", command.strip(), "```", "",
+           "Each counter pass runs `bench.py --pmc-driver`: one step, a torch fp32 negation of 1 GiB into another "
+           "1 GiB (the calibration kernel), then two steps. The calibration kernel reads "
+           f"{fcal:.0f} KiB and writes {wcal:.0f} KiB by the counters, so FETCH_SIZE is scaled by "
+           f"{ff:.4f} and WRITE_SIZE by {wf:.4f}. Values are per-dispatch medians; FETCH_SIZE counts L2 fills "
+           "from the fabric, which include Infinity Cache (MALL) hits.", "",
+           "| kernel | fetch GB | write GB | traffic GB |", "|---|---:|---:|---:|"]
+    machine = []
+    for name in sorted(set(fetch) | set(write)):
+        fb = fetch.get(name, 0.0) * 1024.0 * ff
+        wb = write.get(name, 0.0) * 1024.0 * wf
+        out.append(f"| `{name}` | {fb / 1e9:.3f} | {wb / 1e9:.3f} | {(fb + wb) / 1e9:.3f} |")
+        machine.append(f"traffic {name} fetch_bytes={fb:.0f} write_bytes={wb:.0f}")
+    out += ["", "Machine-readable (read by bench.py for `roofline.traffic`):", "", "```"] + machine + ["```", ""]
+    return "\n".join(out)
+
+
+def stats_summary(directory: str, config: str, command: str) -> str:
+    rows = _csv_rows(directory, "kernel_stats.csv")
+    out = [f"# rocprofv3 kernel stats: {config.upper()}", "", "Command (from the repository root on the MI355X box):",
+           "", "```", command.strip(), "```", "",
+           "| kernel | timer name | calls | total ms | average ms | % of GPU time |",
+           "|---|---|---:|---:|---:|---:|"]
+    other = 0.0
+    for r in rows:
+        name = timer_name(r["Name"])
+        if not name:
+            other += float(r["Percentage"])
+            continue
+        short = r["Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+        out.append(f"| `{short}` | {name} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                   f"{float(r['AverageNs']) / 1e6:.4f} | {float(r['Percentage']):.1f} |")
+    out.append(f"| (torch input generation and copies, outside the timed steps) | | | | | {other:.1f} |")
+    out.append("")
+    return "\n".join(out)
+
+
+def committed_traffic(config: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed traffic summary, or None."""
+    import re
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{PROFILE_PREFIX[config]}_traffic.md")
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(rf"^traffic {re.escape(kernel)} fetch_bytes=(\d+) write_bytes=(\d+)$", text, re.M)
+    if not m:
+        return None
+    return int(m.group(1)) + int(m.group(2)), os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
 
 
 # --------------------------------------------------------------------------- C1
@@ -197,8 +333,33 @@ WORKLOADS = {
 }
 
 
+def pmc_driver(step, device):
+    """One counter pass: one step, the calibration kernel (an elementwise fp32 negation
+    that reads and writes CALIBRATION_BYTES), then two steps."""
+    import torch
+
+    step()
+    torch.cuda.synchronize()
+    src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    print("pmc driver: done", flush=True)
+
+
 def main():
     args = parse()
+    if args.traffic_from:
+        print(traffic_summary(args.traffic_from[0], args.traffic_from[1], args.config, args.command))
+        return
+    if args.stats_from:
+        print(stats_summary(args.stats_from, args.config, args.command))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the "
@@ -218,31 +379,31 @@ def main():
     _lib.load()
     wl = WORKLOADS[args.config](device, args)
     step = wl["step"]
+    if args.pmc_driver:
+        pmc_driver(step, device)
+        return
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    # timed window: exactly K steps between two device synchronisations
+    # timed window: exactly K steps between two device synchronisations.  Kernel
+    # durations come from HIP events the library records around each of its launches,
+    # on the stream the launch uses, inside this same window.
     start_ev, stop_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    start_ev.record()
-    for _ in range(args.steps):
-        step()
-    stop_ev.record()
-    torch.cuda.synchronize()
+    with _lib.KernelTimer() as kt:
+        start_ev.record()
+        for _ in range(args.steps):
+            step()
+        stop_ev.record()
+        torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = start_ev.elapsed_time(stop_ev)
     ms_per_step = gpu_ms / args.steps
     n = wl["n"]
     value = n * args.steps / (gpu_ms / 1e3)
-
-    # kernel durations: HIP events recorded by the library on each launch's stream
-    with _lib.KernelTimer() as kt:
-        for _ in range(args.steps):
-            step()
-    torch.cuda.synchronize()
     kernels = {name: {"launches": c, "mean_ms": tot / max(c, 1)} for name, (c, tot) in kt.times.items()}
     dominant = max(kt.times, key=lambda k: kt.times[k][1])
     dom_ms = kernels[dominant]["mean_ms"]
@@ -256,7 +417,10 @@ def main():
                 "frac": achieved / HBM_PEAK_GBS}
     roof["kernel"] = dominant
     roof["kernel_mean_ms"] = dom_ms
-    roof["traffic"] = None
+    tr = committed_traffic(args.config, dominant)
+    roof["traffic"] = tr[0] if tr else None
+    if tr:
+        roof["traffic_source"] = tr[1]
     fp8_flops = wl.get("kernel_fp8_flops", {})
     for name, info in kernels.items():
         if name in wl["kernel_bytes"]:
