@@ -659,81 +659,186 @@ struct HeadParams {
 
 enum { MODE_STATS = 0, MODE_EMIT = 1, MODE_STORE = 2 };
 
-// Objective epilogue for one token row over this thread's vocab range [vs, vs + nval)
-// of the current tile: zr points at the dumped fp32 logits (LDS), nval is a multiple
-// of 8 (V % 8 == 0).
+// Head-kernel LDS beyond the GEMM stages / epilogue dump: per-token running state and
+// per-token constants of the workgroup's 256 tokens (they persist across vocab tiles).
+constexpr int kStateOff = kDumpLds;                   // [256][8] fp32: mz sz mu su A | arate
+constexpr int kConstOff = kStateOff + 256 * 8 * 4;    // [256][8] fp32: lzl lul cp ct cy
+constexpr int kLabelOff = kConstOff + 256 * 8 * 4;    // [256] int64 labels
+constexpr int kHeadLdsBytes = kLabelOff + 256 * 8;
+static_assert(kHeadLdsBytes <= 160 * 1024, "head kernel LDS");
+static_assert(kGemmLds <= kDumpLds, "the dump region covers the GEMM stages");
+
+// Eight values loaded as raw vectors, unpacked to fp32 later: keeping the unpack away from
+// the load lets all of a row group's loads be in flight together.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<uint16_t> {
+  uint4 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void unpack(float* f) const {
+    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+  }
+};
+template <>
+struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void unpack(float* f) const {
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  }
+};
+
+// Butterfly partner within groups of 8 lanes, by DPP: step 0 swaps lanes 2i <-> 2i+1
+// (quad_perm [1,0,3,2]), step 1 swaps i <-> i^2 inside a quad (quad_perm [2,3,0,1]),
+// step 2 mirrors the 8 lanes (row_half_mirror: i <-> 7-i).  After steps 0 and 1 every
+// lane of a quad holds the same value, so the mirror pairs the two quads exactly as an
+// xor-4 exchange would.
+template <int STEP>
+__device__ __forceinline__ float dpp_partner(float x) {
+  constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : 0x141;
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false));
+}
+
+template <int STEP>
+__device__ __forceinline__ PairState pair_partner(const PairState& a) {
+  return {dpp_partner<STEP>(a.mz), dpp_partner<STEP>(a.sz), dpp_partner<STEP>(a.mu), dpp_partner<STEP>(a.su),
+          dpp_partner<STEP>(a.A)};
+}
+
+// Combine over the 8 lanes of a row group; pair_merge is symmetric, so all 8 lanes end
+// with identical bits.
+__device__ __forceinline__ PairState pair_reduce8(PairState a) {
+  a = pair_merge(a, pair_partner<0>(a));
+  a = pair_merge(a, pair_partner<1>(a));
+  return pair_merge(a, pair_partner<2>(a));
+}
+
+__device__ __forceinline__ float sum_reduce8(float x) {
+  x += dpp_partner<0>(x);
+  x += dpp_partner<1>(x);
+  return x + dpp_partner<2>(x);
+}
+
+// Objective epilogue for one 128-token half of the tile, dumped in LDS as
+// zt[token][vocab] (kZRow floats per token).  Wave w owns tokens 32w .. 32w + 31 of the
+// half in four groups of eight; in a group, lane 8r + c takes token 8g + r and the
+// 16-byte chunks c, c + 8, c + 16, c + 24 of its 256 vocab entries, so each global
+// load or store instruction covers eight rows x 128 contiguous bytes.  The eight lanes
+// of a row combine their partial sums with xor shuffles (a symmetric merge, so every
+// lane ends with the same bits) and lane 0 of the row folds the tile into the token's
+// running state in LDS.  Sums over a tile are formed locally first: one running fp32
+// sum over a whole vocab range (up to ~10^5 terms) would lose the many small terms.
+// V % 8 == 0, so each 8-entry chunk is wholly inside or outside the vocabulary.
 template <int MODE, typename TT>
-__device__ __forceinline__ void epilogue_row(const HeadParams& p, const lds_f32* zr, int64_t t, bool tok_ok,
-                                             int64_t vs, int nval, int64_t y, PairState& st, float& arate,
-                                             float lzl, float lul, float cp, float ct, float cy) {
-  if (nval <= 0) return;
-  const uint16_t* mrow = p.markov ? p.markov + t * p.ldm + vs : nullptr;
-  const TT* urow = static_cast<const TT*>(p.teacher) + t * p.ldt + vs;
-  // Sums over this tile's (at most 128) entries are formed locally and folded into the
-  // running state once per tile: a single running fp32 sum over a whole vocab range
-  // (up to ~10^5 terms per lane) would lose the many small terms to rounding.
-  PairState loc = pair_init();
-  float aloc = 0.f;
-  for (int e = 0; e < nval; e += 16) {
-    const bool second = e + 8 < nval;
-    float z[16], u[16];
+__device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, int half, int64_t t0, int64_t v0) {
+  const lds_f32* zt = reinterpret_cast<const lds_f32*>(lds);
+  lds_f32* state = reinterpret_cast<lds_f32*>(lds + kStateOff);
+  const lds_f32* cst = reinterpret_cast<const lds_f32*>(lds + kConstOff);
+  const __attribute__((address_space(3))) int64_t* lab =
+      reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(lds + kLabelOff);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r8 = lane >> 3, c8 = lane & 7;
+#pragma unroll 1
+  for (int g = 0; g < 4; ++g) {
+    const int tl = 32 * w + 8 * g + r8;      // token within the half
+    const int tk = half * 128 + tl;          // token within the workgroup tile
+    const int64_t t = t0 + tk;
+    const bool tok_ok = t < p.n;
+    const int64_t trow = tok_ok ? t : p.n - 1;
+    const lds_f32* zr = zt + tl * kZRow;
+    const bool has_m = p.markov != nullptr;   // kernel argument: uniform, so no divergent branch
+    const uint16_t* mrow = (has_m ? p.markov : p.weight) + (has_m ? trow * p.ldm + v0 : 0);
+    const TT* urow = MODE == MODE_STORE ? nullptr : static_cast<const TT*>(p.teacher) + trow * p.ldt + v0;
+    float z[32], u[32];
+    bool ok[4];
+    // loads are unconditional (chunks past V re-read the row's first chunk) and the
+    // values are masked afterwards, so all of them are in flight together
+    Raw8<uint16_t> mraw[4];
+    Raw8<TT> uraw[4];
+    int vc[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4_t x = *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(zr + e + 4 * q);
-      z[4 * q] = x[0]; z[4 * q + 1] = x[1]; z[4 * q + 2] = x[2]; z[4 * q + 3] = x[3];
+    for (int k = 0; k < 4; ++k) {
+      const int vl = 8 * c8 + 64 * k;
+      ok[k] = v0 + vl < p.v;
+      vc[k] = ok[k] ? vl : 0;
+      if (MODE != MODE_STORE) uraw[k].load(urow + vc[k]);
     }
-    if (mrow) {
-      float mk[16];
-      load8(mrow + e, mk);
-      if (second) load8(mrow + e + 8, mk + 8);
+    if (has_m) {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) z[q] += (q < 8 || second) ? mk[q] : 0.f;
+      for (int k = 0; k < 4; ++k) mraw[k].load(mrow + vc[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int vl = 8 * c8 + 64 * k;
+      const f32x4_t x0 = *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(zr + vl);
+      const f32x4_t x1 = *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(zr + vl + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { z[8 * k + e] = x0[e]; z[8 * k + 4 + e] = x1[e]; }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float mk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (has_m) mraw[k].unpack(mk);
+      if (MODE != MODE_STORE) uraw[k].unpack(u + 8 * k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        z[8 * k + e] = ok[k] ? z[8 * k + e] + mk[e] : kNegBig;
+        if (MODE != MODE_STORE) u[8 * k + e] = ok[k] ? u[8 * k + e] : kNegBig;
+      }
     }
     if (MODE == MODE_STORE) {
-      if (tok_ok) {
-        store8(p.out + t * p.ldo + vs + e, z);
-        if (second) store8(p.out + t * p.ldo + vs + e + 8, z + 8);
-      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (ok[k] && tok_ok) store8(p.out + t * p.ldo + v0 + 8 * c8 + 64 * k, z + 8 * k);
       continue;
     }
-    load8(urow + e, u);
-    if (second) {
-      load8(urow + e + 8, u + 8);
-    } else {
-#pragma unroll
-      for (int q = 8; q < 16; ++q) { z[q] = kNegBig; u[q] = kNegBig; }
-    }
+    const int64_t y = lab[tk];
+    const int64_t yr = y - v0;
+    // this lane holds z_y (labels outside [0, V) match nothing; the merge flags them)
+    const bool mine = yr >= 0 && yr < BM && y < p.v && ((yr >> 3) & 7) == c8 && tok_ok;
     if (MODE == MODE_STATS) {
-      pair_update<16>(loc, z, u);
+      PairState loc = pair_init();
+      // ok[] falls with k: a lane with no valid chunk keeps the empty state (an update
+      // with every entry at the sentinel would form inf - inf)
+      if (ok[0]) pair_update<32>(loc, z, u);
+      loc = pair_reduce8(loc);
+      if (c8 == 0) {
+        lds_f32* sr = state + tk * 8;
+        const PairState r = pair_merge(PairState{sr[0], sr[1], sr[2], sr[3], sr[4]}, loc);
+        sr[0] = r.mz; sr[1] = r.sz; sr[2] = r.mu; sr[3] = r.su; sr[4] = r.A;
+      }
+      if (mine) p.zy[t] = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
     } else {
-      float d[16];
+      const lds_f32* cr = cst + tk * 8;
+      const float lzl = cr[0], lul = cr[1], cp = cr[2], ct = cr[3], cy = cr[4];
+      float aloc = 0.f;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const float pp = fast_exp2(__builtin_fmaf(z[q], kLog2e, -lzl));
-        const float tt = fast_exp2(__builtin_fmaf(u[q], kLog2e, -lul));
-        aloc += fminf(pp, tt);
-        d[q] = __builtin_fmaf(cp, pp, -ct * tt);
+      for (int k = 0; k < 4; ++k) {
+        float d[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pp = fast_exp2(__builtin_fmaf(z[8 * k + e], kLog2e, -lzl));
+          const float tt = fast_exp2(__builtin_fmaf(u[8 * k + e], kLog2e, -lul));
+          aloc += fminf(pp, tt);
+          d[e] = __builtin_fmaf(cp, pp, -ct * tt);
+        }
+        if (p.dl && ok[k] && tok_ok) store8(p.dl + t * p.ldd + v0 + 8 * c8 + 64 * k, d);
       }
-      if (p.dl && tok_ok) {
-        store8(p.dl + t * p.ldd + vs + e, d);
-        if (second) store8(p.dl + t * p.ldd + vs + e + 8, d + 8);
+      aloc = sum_reduce8(aloc);
+      if (c8 == 0) state[tk * 8] += aloc;
+      // the label entry: rewrite dl[y] with the -c_ce term (same lane, after its store)
+      if (mine && p.dl) {
+        const float zy = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
+        const float uy = load1(urow + yr);
+        const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
+        const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
+        store1(p.dl + t * p.ldd + y, __builtin_fmaf(cp, pp, -ct * tt) - cy);
       }
-    }
-  }
-  if (MODE == MODE_STORE) return;
-  if (MODE == MODE_STATS) st = pair_merge(st, loc);
-  else arate += aloc;
-  // the label entry: pass 1 records z_y, pass 2 rewrites dl[y] with the -c_ce term
-  const int64_t yr = y - vs;
-  if (yr >= 0 && yr < nval && tok_ok) {
-    const float zy = zr[yr] + (mrow ? bf16_to_f32(mrow[yr]) : 0.f);
-    if (MODE == MODE_STATS) {
-      p.zy[t] = zy;
-    } else if (p.dl) {
-      const float uy = load1(urow + yr);
-      const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
-      const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
-      store1(p.dl + t * p.ldd + vs + yr, __builtin_fmaf(cp, pp, -ct * tt) - cy);
     }
   }
 }
@@ -743,36 +848,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 void head_kernel(HeadParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_t* lds = (lds_t*)lds_raw;
-  lds_f32* zt = reinterpret_cast<lds_f32*>(lds);
   int tile_t, split;
   wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, tile_t, split);
   const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
   const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
   const int tid = threadIdx.x;
   const int wn = (tid >> 6) & 1;
-  const int tl = tid & 127, hh = tid >> 7;   // epilogue: token row in the half, vocab half
   const int64_t t0 = (int64_t)tile_t * BN;
 
-  // this thread's two epilogue tokens (one per 128-token half) and their constants
-  int64_t trow[2], ylab[2] = {0, 0};
-  bool tok_ok[2];
-  PairState st[2];
-  float arate[2] = {0.f, 0.f};
-  float lzl[2] = {0.f, 0.f}, lul[2] = {0.f, 0.f}, cp[2] = {0.f, 0.f}, ct[2] = {0.f, 0.f}, cy[2] = {0.f, 0.f};
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    const int64_t t = t0 + jj * 128 + tl;
-    tok_ok[jj] = t < p.n;
-    trow[jj] = tok_ok[jj] ? t : p.n - 1;
-    st[jj] = pair_init();
-    if (MODE != MODE_STORE) ylab[jj] = p.labels[trow[jj]];
+  // per-token state and constants of this workgroup's 256 tokens (thread tid: token tid);
+  // first read after the GEMM's barriers
+  if (MODE != MODE_STORE) {
+    const int64_t t = t0 + tid;
+    const int64_t trow = t < p.n ? t : p.n - 1;
+    lds_f32* sr = reinterpret_cast<lds_f32*>(lds + kStateOff) + tid * 8;
+    const PairState z0 = pair_init();
+    sr[0] = MODE == MODE_STATS ? z0.mz : 0.f;
+    sr[1] = z0.sz; sr[2] = z0.mu; sr[3] = z0.su; sr[4] = z0.A;
+    reinterpret_cast<__attribute__((address_space(3))) int64_t*>(lds + kLabelOff)[tid] = p.labels[trow];
     if (MODE == MODE_EMIT) {
-      lzl[jj] = p.row_stats[trow[jj] * kRowStatWidth + kLseZ] * kLog2e;
-      lul[jj] = p.row_stats[trow[jj] * kRowStatWidth + kLseU] * kLog2e;
-      const float w = p.weights[trow[jj]] * p.inv_acc;
-      cp[jj] = w * (p.c_ce + p.c_kl);
-      ct[jj] = w * p.c_kl;
-      cy[jj] = w * p.c_ce;
+      lds_f32* cr = reinterpret_cast<lds_f32*>(lds + kConstOff) + tid * 8;
+      const float w = p.weights[trow] * p.inv_acc;
+      cr[0] = p.row_stats[trow * kRowStatWidth + kLseZ] * kLog2e;
+      cr[1] = p.row_stats[trow * kRowStatWidth + kLseU] * kLog2e;
+      cr[2] = w * (p.c_ce + p.c_kl);
+      cr[3] = w * p.c_kl;
+      cr[4] = w * p.c_ce;
     }
   }
 
@@ -781,45 +882,27 @@ void head_kernel(HeadParams p) {
     const int64_t v0 = (int64_t)vt * BM;
     zero_acc(acc);
     gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds);
-    const int64_t vs = v0 + hh * 128;
-    const int64_t rem = p.v - vs;
-    const int nval = rem >= 128 ? 128 : (rem > 0 ? (int)rem : 0);
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       if (wn == jj) dump_half(acc, lds);
       __syncthreads();
-      epilogue_row<MODE, TT>(p, zt + tl * kZRow + hh * 128, trow[jj], tok_ok[jj], vs, nval, ylab[jj], st[jj],
-                             arate[jj], lzl[jj], lul[jj], cp[jj], ct[jj], cy[jj]);
+      epilogue_half<MODE, TT>(p, lds, jj, t0, v0);
       __syncthreads();
     }
   }
 
   if (MODE == MODE_STORE) return;
-  // combine the two vocab halves of every token and write this split's partial
-  lds_f32* red = zt;   // [2 halves][256 tokens][5]
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    lds_f32* dst = red + (hh * 256 + jj * 128 + tl) * 5;
-    if (MODE == MODE_STATS) {
-      dst[0] = st[jj].mz; dst[1] = st[jj].sz; dst[2] = st[jj].mu; dst[3] = st[jj].su; dst[4] = st[jj].A;
-    } else {
-      dst[0] = arate[jj];
-    }
-  }
-  __syncthreads();
+  // this split's partial of every token (state complete: the last epilogue ended with a barrier)
   const int64_t t = t0 + tid;
   if (t < p.n) {
-    const lds_f32* a = red + tid * 5;
-    const lds_f32* b = red + (256 + tid) * 5;
+    const lds_f32* sr = reinterpret_cast<const lds_f32*>(lds + kStateOff) + tid * 8;
     if (MODE == MODE_STATS) {
-      const PairState r = pair_merge(PairState{a[0], a[1], a[2], a[3], a[4]},
-                                     PairState{b[0], b[1], b[2], b[3], b[4]});
       RowPart rp;
-      rp.mz = r.mz; rp.sz = r.sz; rp.mu = r.mu; rp.su = r.su; rp.A = r.A;
+      rp.mz = sr[0]; rp.sz = sr[1]; rp.mu = sr[2]; rp.su = sr[3]; rp.A = sr[4];
       rp.pad0 = rp.pad1 = rp.pad2 = 0.f;
       p.part1[t * p.splits + split] = rp;
     } else {
-      p.parta[t * p.splits + split] = a[0] + b[0];
+      p.parta[t * p.splits + split] = sr[0];
     }
   }
 }
@@ -1015,12 +1098,12 @@ hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<MODE, TT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHeadLdsBytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   NS_TIMED(name, st);
-  hipLaunchKernelGGL((head_kernel<MODE, TT>), dim3(grid), dim3(kThreads), kLdsBytes, st, p);
+  hipLaunchKernelGGL((head_kernel<MODE, TT>), dim3(grid), dim3(kThreads), kHeadLdsBytes, st, p);
   return hipGetLastError();
 }
 
