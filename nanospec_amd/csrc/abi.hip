@@ -195,7 +195,7 @@ int ns_fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t
   if ((rc = check_matrix(wq, v, d, ldw, "wq"))) return rc;
   if ((rc = check_matrix(out, n, v, ldo, "out"))) return rc;
   if (!scale) return fail(NS_ENULL, "scale is NULL");
-  if (!aligned(x) || !aligned(wq) || !aligned(out) || ldx % 8 || ldw % 16 || ldo % 4)
+  if (!aligned(x) || !aligned(wq) || !aligned(out) || ldx % 8 || ldw % 16 || ldo % 8)
     return fail(NS_EALIGN, "fp8 head needs 16-byte aligned base pointers and rows");
   const size_t need = ns::fp8_workspace_bytes(n, d);
   if (n > 0 && (!workspace || workspace_bytes < need))

@@ -7,6 +7,9 @@
 // The block dot products run on gfx950's fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4 with
 // unit e8m0 scales): e4m3 x e4m3 products are exact in fp32, so only the fp32
 // accumulation order differs from the reference's dequantise-then-fp32-GEMM.
+#include <type_traits>
+
+#include "ns_gemm.h"
 #include "ns_internal.h"
 #include "ns_profile.h"
 
@@ -14,17 +17,8 @@ namespace ns {
 namespace {
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) char lds_t;
 
 constexpr int kQBlock = 128;     // quantisation block (K) and weight-scale block (rows, K)
-constexpr int TM = 128;          // vocab rows per workgroup tile (one weight-scale row block)
-constexpr int TN = 128;          // tokens per workgroup tile
-constexpr int kThreads = 256;    // 4 waves as 2 (vocab) x 2 (tokens), 64 x 64 each
-constexpr int kTileBytes = TM * kQBlock;         // 16 KB per operand per stage
-constexpr int kLdsBytes = 4 * kTileBytes;        // 2 stages x 2 operands = 64 KB
-constexpr int kNumXcd = 8;
 
 // float in [-448, 448] -> OCP e4m3 (fn) code, round to nearest even; -0 keeps its sign.
 __device__ __forceinline__ uint32_t e4m3_code(float x) {
@@ -64,9 +58,6 @@ __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restri
   if (lane == 0) xs[row * nb + kb] = s;
 }
 
-__device__ __forceinline__ int swz(int row) { return ((row & 7) + ((row >> 3) & 1)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ swz(row)) << 4); }
-
 struct Fp8Params {
   const uint8_t* qx;       // [N, d] e4m3 codes (row stride d)
   const float* xs;         // [N, d/128]
@@ -76,132 +67,237 @@ struct Fp8Params {
   uint16_t* out;           // [N, V] bf16
   int64_t ldo;
   int64_t n, v, d;
-  int vt, tt;              // vocab tiles, token tiles
+  int tt, vt, splits, xa;  // token tiles, vocab tiles, vocab splits, XCD block (wg_coords)
 };
 
-// 128 rows x 128 bytes tile -> registers (4 x 16 B per thread), rows >= rmax clamped.
-__device__ __forceinline__ void load_rows(uint4 (&r)[4], const uint8_t* base, int64_t ld, int64_t r0,
-                                          int64_t rmax, int64_t k0) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int64_t row = r0 + i * 32 + (tid >> 3);
-    row = row < rmax ? row : rmax - 1;
-    r[i] = *reinterpret_cast<const uint4*>(base + row * ld + k0 + (tid & 7) * 16);
-  }
+// Workgroup tile: 256 vocab rows (two weight-scale row blocks) x 128 tokens, 4 waves as
+// 2 (vocab) x 2 (tokens), each 128 x 64 = 4 x 2 blocks of 32 x 32.  K advances one
+// 128-entry quantisation block per stage; stages live in a 3-deep LDS ring so the fills
+// of stage t + 2 can be issued anywhere in stage t.
+constexpr int FM = 256;
+constexpr int FN = 128;
+constexpr int kThreads = 256;
+constexpr int kAStage = FM * kQBlock;        // 32 KB of weight codes
+constexpr int kBStage = FN * kQBlock;        // 16 KB of activation codes
+constexpr int kStage = kAStage + kBStage;
+constexpr int kRing = 3;
+constexpr int kFp8Lds = kRing * kStage;      // 144 KB
+constexpr int kOutRow = FM * 2 + 16;         // bf16 output row in the LDS transpose (+16 B)
+static_assert(FN * kOutRow <= kFp8Lds, "output transpose fits in the ring");
+
+// s_waitcnt vmcnt(12) lgkmcnt(0) (expcnt not waited): gfx9 encoding, vmcnt[3:0] in bits
+// 3:0, expcnt in 6:4, lgkmcnt in 11:8, vmcnt[5:4] in 15:14.
+constexpr int kWaitStage = 12 | (7 << 4);
+
+__device__ __forceinline__ u32x4_t rd16(const lds_t* base, int row, int chunk) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(base + lds_off(row, chunk));
 }
 
-__device__ __forceinline__ void store_rows(const uint4 (&r)[4], lds_t* lds) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = i * 32 + (tid >> 3);
-    const u32x4_t y = {r[i].x, r[i].y, r[i].z, r[i].w};
-    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(lds + lds_off(row, tid & 7)) = y;
-  }
-}
-
-// 32 fp8 K-entries (two 16-byte chunks) of LDS row `row` for MFMA K-half `kk`.
-__device__ __forceinline__ i32x8_t frag(const lds_t* base, int row, int kk, int kh) {
-  const int c = kk * 4 + kh * 2;
-  const u32x4_t lo = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(base + lds_off(row, c));
-  const u32x4_t hi = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(base + lds_off(row, c + 1));
+__device__ __forceinline__ i32x8_t join(const u32x4_t& lo, const u32x4_t& hi) {
   i32x8_t r;
   r[0] = (int)lo[0]; r[1] = (int)lo[1]; r[2] = (int)lo[2]; r[3] = (int)lo[3];
   r[4] = (int)hi[0]; r[5] = (int)hi[1]; r[6] = (int)hi[2]; r[7] = (int)hi[3];
   return r;
 }
 
-__global__ __launch_bounds__(kThreads) void fp8_head_kernel(Fp8Params p) {
+// One fp8 MFMA block product: 32 x 32 outputs over 64 K-entries.  Operand lane layout:
+// lane r + 32 kh holds row r, K entries 32 kh .. 32 kh + 31 of the 64 (two 16-byte
+// chunks); unit e8m0 scales (127).
+__device__ __forceinline__ f32x16_t mfma_f8(const u32x4_t (&a)[2], const u32x4_t (&b)[2], const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(join(a[0], a[1]), join(b[0], b[1]), c, 0, 0, 0, 127, 0,
+                                                          127);
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fp8_head_kernel(Fp8Params p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_t* lds = (lds_t*)lds_raw;
-  const int G = gridDim.x;
-  int L = blockIdx.x;
-  if (G % kNumXcd == 0) L = (L % kNumXcd) * (G / kNumXcd) + L / kNumXcd;
-  const int tt = L % p.tt, vt = L / p.tt;   // consecutive ids share the weight tile
-  const int64_t v0 = (int64_t)vt * TM, t0 = (int64_t)tt * TN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int r = lane & 31, kh = lane >> 5;
+  int tile_t, split;
+  wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, tile_t, split);
+  const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
+  const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lane = tid & 63, r = lane & 31, kh = lane >> 5;
   const int KB = (int)(p.d / kQBlock);
-  const float* wsrow = p.ws + (int64_t)vt * KB;     // the tile is one weight-scale row block
+  const int64_t t0 = (int64_t)tile_t * FN;
+  const int nvb = (int)(p.v / kQBlock);
+  auto buf = [&](int t) -> lds_t* { return lds + (t % kRing) * kStage; };
+  auto clampk = [&](int t) -> int64_t { return (int64_t)(t < KB - 1 ? t : KB - 1) * kQBlock; };
 
-  int64_t tok[2];
+  DmaTile<FN> tb;
+  tb.init(p.d, t0, p.n, wv);
+  const char* pb = reinterpret_cast<const char*>(p.qx + t0 * p.d);
+  const float* xsrow[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t t = t0 + wn * 64 + j * 32 + r;
-    tok[j] = t < p.n ? t : p.n - 1;
+    xsrow[j] = p.xs + (t < p.n ? t : p.n - 1) * KB;
   }
 
-  f32x16_t acc[2][2];
+  for (int vt = vt_begin; vt < vt_end; ++vt) {
+    const int64_t v0 = (int64_t)vt * FM;
+    DmaTile<FM> ta;
+    ta.init(p.ldw, v0, p.v, wv);
+    const char* pa = reinterpret_cast<const char*>(p.wq + v0 * p.ldw);
+    int vb = (int)(v0 / kQBlock) + wm;   // this wave's weight-scale row block
+    vb = vb < nvb ? vb : nvb - 1;        // a tile half past V: rows discarded
+    const float* wsrow = p.ws + (int64_t)vb * KB;
+
+    f32x16_t acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[q][j][e] = 0.f;
+
+    // prologue: stages 0 and 1 in flight, stage 0's scales, then stage 0's fragments
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ta.issue(pa, buf(0), wv, i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tb.issue(pb, buf(0) + kAStage, wv, i);
+    {
+      const int64_t k1 = clampk(1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ta.issue(pa + k1, buf(1), wv, i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tb.issue(pb + k1, buf(1) + kAStage, wv, i);
+    }
+    float c_cur[2], c_prev[2] = {0.f, 0.f}, xn[2], wnx;
+    {
+      const float w0 = wsrow[0];
+      c_cur[0] = xsrow[0][0] * w0;
+      c_cur[1] = xsrow[1][0] * w0;
+    }
+    fill_barrier();
+    u32x4_t a[2][2][2];      // [q parity][kk][chunk half]
+    u32x4_t b[2][2][2][2];   // [stage parity][j][kk][chunk half]
+    f32x16_t part[2][2];     // [q parity][j]
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          b[0][j][kk][h] = rd16(buf(0) + kAStage, wn * 64 + j * 32 + r, kk * 4 + kh * 2 + h);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) a[0][kk][h] = rd16(buf(0), wm * 128 + r, kk * 4 + kh * 2 + h);
 
-  uint4 ra[4], rb[4];
-  load_rows(ra, p.wq, p.ldw, v0, p.v, 0);
-  load_rows(rb, p.qx, p.d, t0, p.n, 0);
-  store_rows(ra, lds);
-  store_rows(rb, lds + kTileBytes);
-  __syncthreads();
-  if (KB > 1) {
-    load_rows(ra, p.wq, p.ldw, v0, p.v, kQBlock);
-    load_rows(rb, p.qx, p.d, t0, p.n, kQBlock);
-  }
-  for (int kb = 0; kb < KB; ++kb) {
-    const lds_t* la = lds + (kb & 1) * 2 * kTileBytes;
-    const lds_t* lb = la + kTileBytes;
-    const float sw = wsrow[kb];
-    float c[2];
+    // one stage; the parity SP of the B fragment buffers is a compile-time constant so
+    // the fragment arrays stay in registers
+    auto stage = [&](int t, auto spc) {
+      constexpr int sp = decltype(spc)::value;
+      const lds_t* cb = buf(t);
+      const lds_t* nb = buf(t + 1);
+      lds_t* db = buf(t + 2);
+      const int64_t k2 = clampk(t + 2);
+      const int kn = t + 1 < KB ? t + 1 : KB - 1;
+      // 16 MFMA slots: s = 4 q + 2 kk + j; between them, one or more of the stage's other
+      // operations (sched_barrier keeps the order)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) c[j] = p.xs[tok[j] * KB + kb] * sw;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        f32x16_t part = {};
+      for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const i32x8_t a = frag(la, wm * 64 + i * 32 + r, kk, kh);
-          const i32x8_t b = frag(lb, wn * 64 + j * 32 + r, kk, kh);
-          part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, part, 0, 0, 0, 127, 0, 127);
-        }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(c[j], part[e], acc[i][j][e]);
+          for (int j = 0; j < 2; ++j) {
+            const int s = 4 * q + 2 * kk + j;
+            part[q & 1][j] = mfma_f8(a[q & 1][kk], b[sp][j][kk], kk == 0 ? f32x16_t{} : part[q & 1][j]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s == 0) {   // next stage's scales (complete by this stage's barrier)
+              xn[0] = xsrow[0][kn];
+              xn[1] = xsrow[1][kn];
+              wnx = wsrow[kn];
+            }
+            if (s < 8) ta.issue(pa + k2, db, wv, s);
+            else if (s < 12) tb.issue(pb + k2, db + kAStage, wv, s - 8);
+            if (q < 3) {     // block row q + 1's A fragments, one chunk per slot
+              const int p4 = s & 3;
+              a[(q + 1) & 1][p4 >> 1][p4 & 1] =
+                  rd16(cb, wm * 128 + (q + 1) * 32 + r, (p4 >> 1) * 4 + kh * 2 + (p4 & 1));
+            }
+            // fold block (q - 1, j') into the accumulator, 8 elements per slot; slots of
+            // q = 0 fold the previous stage's block row 3
+            {
+              const int jj = (s & 3) >> 1, e0 = (s & 1) * 8;
+              if (q > 0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  acc[q - 1][jj][e0 + e] = __builtin_fmaf(c_cur[jj], part[(q - 1) & 1][jj][e0 + e], acc[q - 1][jj][e0 + e]);
+              } else if (t > 0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  acc[3][jj][e0 + e] = __builtin_fmaf(c_prev[jj], part[1][jj][e0 + e], acc[3][jj][e0 + e]);
+              }
+            }
+            if (s == 11) {   // stage t + 1 landed everywhere; buffer t free after this
+              asm volatile("" ::: "memory");
+              __builtin_amdgcn_s_waitcnt(kWaitStage);
+              __builtin_amdgcn_s_barrier();
+              asm volatile("" ::: "memory");
+            }
+            if (q == 3) {    // stage t + 1's fragments: B (8 chunks) and A row 0 (4)
+              const int u = s - 12;
+#pragma unroll
+              for (int m = 0; m < 3; ++m) {
+                const int o = 3 * u + m;   // 0..11
+                if (o < 8) {
+                  const int j2 = o >> 2, kk2 = (o >> 1) & 1, h2 = o & 1;
+                  b[sp ^ 1][j2][kk2][h2] = rd16(nb + kAStage, wn * 64 + j2 * 32 + r, kk2 * 4 + kh * 2 + h2);
+                } else {
+                  const int o4 = o - 8;
+                  a[0][o4 >> 1][o4 & 1] = rd16(nb, wm * 128 + r, (o4 >> 1) * 4 + kh * 2 + (o4 & 1));
+                }
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
       }
+      c_prev[0] = c_cur[0];
+      c_prev[1] = c_cur[1];
+      c_cur[0] = xn[0] * wnx;
+      c_cur[1] = xn[1] * wnx;
+    };
+    for (int t = 0; t < KB; t += 2) {
+      stage(t, std::integral_constant<int, 0>{});
+      if (t + 1 < KB) stage(t + 1, std::integral_constant<int, 1>{});
     }
-    if (kb + 1 < KB) {
-      lds_t* nxt = lds + ((kb + 1) & 1) * 2 * kTileBytes;
-      store_rows(ra, nxt);
-      store_rows(rb, nxt + kTileBytes);
+    // the last stage's block row 3
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[3][j][e] = __builtin_fmaf(c_prev[j], part[1][j][e], acc[3][j][e]);
+    fill_barrier();   // no fill in flight, every wave done with the ring
+
+    // bf16 tile transposed through LDS, then whole 16-byte chunks of output rows
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int tl = wn * 64 + j * 32 + r;
+          const int vl = wm * 128 + q * 32 + 8 * g + 4 * kh;
+          const u32x2_t y = {pack_bf16x2(acc[q][j][4 * g], acc[q][j][4 * g + 1]),
+                             pack_bf16x2(acc[q][j][4 * g + 2], acc[q][j][4 * g + 3])};
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + tl * kOutRow + vl * 2) = y;
+        }
+    __syncthreads();
+#pragma unroll 4
+    for (int i = 0; i < FN * (FM / 8) / kThreads; ++i) {
+      const int ci = i * kThreads + tid;
+      const int row = ci >> 5, c16 = ci & 31;
+      const int64_t t = t0 + row, v = v0 + c16 * 8;
+      if (t < p.n && v < p.v) {
+        const u32x4_t x = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + row * kOutRow + c16 * 16);
+        *reinterpret_cast<uint4*>(p.out + t * p.ldo + v) = make_uint4(x[0], x[1], x[2], x[3]);
+      }
     }
     __syncthreads();
-    if (kb + 2 < KB) {
-      load_rows(ra, p.wq, p.ldw, v0, p.v, (int64_t)(kb + 2) * kQBlock);
-      load_rows(rb, p.qx, p.d, t0, p.n, (int64_t)(kb + 2) * kQBlock);
-    }
-  }
-
-  const int h = lane >> 5;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t t = t0 + wn * 64 + j * 32 + r;
-    if (t >= p.n) continue;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t v = v0 + wm * 64 + i * 32 + 8 * g + 4 * h;
-        if (v < p.v) {
-          uint2 o;
-          o.x = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
-          o.y = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-          *reinterpret_cast<uint2*>(p.out + t * p.ldo + v) = o;
-        }
-      }
   }
 }
 
@@ -234,17 +330,24 @@ hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int
   p.qx = qx; p.xs = xs; p.wq = wq; p.ws = scale; p.ldw = ldw;
   p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
   p.n = n; p.v = v; p.d = d;
-  p.vt = (int)((v + TM - 1) / TM);
-  p.tt = (int)((n + TN - 1) / TN);
+  p.vt = (int)((v + FM - 1) / FM);
+  p.tt = (int)((n + FN - 1) / FN);
+  int cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  int sp = (cus + p.tt - 1) / p.tt;
+  sp = sp < 1 ? 1 : (sp > p.vt ? p.vt : sp);
+  p.splits = sp;
+  p.xa = xcd_block(p.tt, sp);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_head_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kFp8Lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   NS_TIMED("fp8_head_gemm", st);
-  hipLaunchKernelGGL(fp8_head_kernel, dim3((unsigned)(p.vt * p.tt)), dim3(kThreads), kLdsBytes, st, p);
+  hipLaunchKernelGGL(fp8_head_kernel, dim3((unsigned)(p.tt * sp)), dim3(kThreads), kFp8Lds, st, p);
   return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@
 // buffered with an XOR swizzle on 16-byte chunks, persistent workgroups that walk a
 // contiguous vocab range with per-token running statistics, and a workgroup -> tile map
 // that puts the workgroups sharing a W stream on the same XCD (shared L2).
+#include "ns_gemm.h"
 #include "ns_internal.h"
 #include "ns_profile.h"
 
@@ -25,10 +26,6 @@ namespace ns {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) char lds_t;   // LDS byte pointer
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 256;          // MFMA rows per workgroup tile
 constexpr int BN = 256;          // MFMA columns per workgroup tile
@@ -39,15 +36,8 @@ constexpr int kGemmLds = 4 * kStageBytes;   // 2 stages x 2 operands = 128 KB
 constexpr int kZRow = BM + 4;               // padded fp32 row of the epilogue dump
 constexpr int kDumpLds = 128 * kZRow * 4;   // 128 token rows x 256 vocab fp32
 constexpr int kLdsBytes = kGemmLds > kDumpLds ? kGemmLds : kDumpLds;
-constexpr int kNumXcd = 8;
 
-typedef __attribute__((address_space(3))) float lds_f32;
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// 16-byte chunk swizzle: rows r and r+8 rotate, so 8- and 16-lane groups reading one
-// logical chunk of consecutive rows hit distinct banks.
-__device__ __forceinline__ int swz(int row) { return ((row & 7) + ((row >> 3) & 1)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ swz(row)) << 4); }
 
 // Per-lane byte offsets of a 256 (rows) x 64 (K) bf16 tile of a K-contiguous matrix,
 // relative to the uniform address of element (r0, k0).  Thread t loads rows
@@ -262,43 +252,6 @@ __device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la
   }
 }
 
-// One 256-row operand tile fetched straight into LDS (global_load_lds_dwordx4): wave wv
-// issues 8 instructions per stage, instruction i filling the 1 KB LDS block wv * 8 + i,
-// i.e. rows 8 (wv * 8 + i) .. +8.  Lane l writes the block's 16-byte slot l, which is
-// physical chunk l % 8 of row 8 (wv * 8 + i) + l / 8; the lane therefore fetches the
-// logical chunk (l % 8) ^ swz(row), so the tile lands in the swizzled lds_off layout.
-// Rows past rmax re-read row rmax - 1 (their results are discarded by the caller).
-struct DmaTile {
-  uint32_t off[8];  // per-lane byte offsets from the tile's first row, stage 0
-  __device__ __forceinline__ void init(int64_t ld, int64_t r0, int64_t rmax, int wv) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = (wv * 8 + i) * 8 + (lane >> 3);
-      int64_t r = r0 + row;
-      r = r < rmax ? r : rmax - 1;
-      const int chunk = (lane & 7) ^ swz(row);
-      off[i] = (uint32_t)(((r - r0) * ld + chunk * 8) * 2);
-    }
-  }
-  // instruction i of one stage: `base` = the tile's first row at this stage's K offset,
-  // `dst` = the operand's LDS stage buffer (wave-uniform)
-  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
-                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * 8 + i) * 1024),
-                                     16, 0, 0);
-  }
-};
-
-// Wait for this wave's LDS fills and all outstanding memory operations, then a
-// workgroup barrier.  The empty asm statements keep the compiler from moving memory
-// accesses across the barrier.
-__device__ __forceinline__ void fill_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T, both row-major with K contiguous and
 // K a multiple of BK.  Ends with a barrier (LDS free for the caller).
@@ -317,9 +270,9 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
                                         int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
   const int KT = (int)(K / BK);
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  DmaTile ta, tb;
-  ta.init(lda, a0, amax, wv);
-  tb.init(ldb, b0, bmax, wv);
+  DmaTile<256> ta, tb;
+  ta.init(lda * 2, a0, amax, wv);
+  tb.init(ldb * 2, b0, bmax, wv);
   const char* pa = reinterpret_cast<const char*>(A + a0 * lda);
   const char* pb = reinterpret_cast<const char*>(B + b0 * ldb);
   auto stage_k = [&](int t) -> int64_t { return (int64_t)(t < KT - 1 ? t : KT - 1) * BK * 2; };
@@ -450,9 +403,9 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
                                             int64_t ldb, int64_t c0, int64_t cmax, int64_t k0, int KT,
                                             lds_t* lds) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  DmaTile ta;
+  DmaTile<256> ta;
   DmaTileKN tb;
-  ta.init(lda, a0, amax, wv);
+  ta.init(lda * 2, a0, amax, wv);
   tb.init(ldb, c0, cmax, wv);
   const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
   const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
@@ -612,26 +565,6 @@ __device__ __forceinline__ void dump_half(const f32x16_t (&acc)[4][4], lds_t* ld
       }
 }
 
-// Workgroup -> (token tile, vocab split) map.  Workgroups are dispatched round-robin over
-// the 8 XCDs, and the C = G / 8 workgroups of one XCD share its L2.  With xa > 0 each
-// XCD holds a block of xa token tiles x (C / xa) vocab splits, so one K stage of the
-// block reads xa + C / xa distinct operand tiles through that L2 (12 for a 4 x 8 block,
-// against 18 for 16 token tiles x 2 splits).  xa = 0: consecutive ids per XCD, token
-// tile fastest.
-__device__ __forceinline__ void wg_coords(int g, int G, int TT, int xa, int& t, int& s) {
-  if (xa > 0) {
-    const int C = G / kNumXcd, xb = C / xa;
-    const int x = g % kNumXcd, r = g / kNumXcd;
-    const int groups_t = TT / xa;
-    t = (x % groups_t) * xa + r % xa;
-    s = (x / groups_t) * xb + r / xa;
-    return;
-  }
-  int L = g;
-  if (G % kNumXcd == 0) L = (g % kNumXcd) * (G / kNumXcd) + g / kNumXcd;
-  s = L / TT;
-  t = L % TT;
-}
 
 // ------------------------------------------------------------------ head kernel
 
@@ -1012,20 +945,6 @@ struct HeadPlan {
   int xa;  // token tiles per XCD block, 0 = unblocked (wg_coords)
 };
 
-// Token tiles per XCD block for a tt x splits grid: a divisor a of C = grid / 8 with
-// tt % a == 0 and splits % (C / a) == 0, minimising a + C / a (distinct operand tiles
-// per K stage in one L2); 0 when no such block exists.
-int xcd_block(int tt, int splits) {
-  const int grid = tt * splits;
-  if (grid % kNumXcd) return 0;
-  const int C = grid / kNumXcd;
-  int best = 0;
-  for (int a = 1; a <= C; ++a) {
-    if (C % a || tt % a || splits % (C / a)) continue;
-    if (best == 0 || a + C / a < best + C / best) best = a;
-  }
-  return best;
-}
 
 HeadPlan head_plan(int64_t n, int64_t v) {
   HeadPlan pl;

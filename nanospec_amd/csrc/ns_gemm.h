@@ -1,0 +1,104 @@
+// Building blocks shared by the MFMA GEMM kernels (lmhead.hip, fp8.hip): the swizzled
+// LDS tile layout, direct-to-LDS operand fills, the fill barrier and the XCD-aware
+// workgroup -> tile maps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ns {
+
+typedef __attribute__((address_space(3))) char lds_t;   // LDS byte pointer
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kNumXcd = 8;   // MI355X: 8 XCDs, workgroups dispatched round-robin over them
+
+// LDS tiles hold rows of 128 bytes (64 bf16 or 128 fp8 K-entries) as eight 16-byte
+// chunks.  Swizzle: chunk c of row r sits at c ^ swz(r); rows r and r + 8 rotate, so 8-
+// and 16-lane groups reading one logical chunk of consecutive rows hit distinct banks.
+__device__ __forceinline__ int swz(int row) { return ((row & 7) + ((row >> 3) & 1)) & 7; }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ swz(row)) << 4); }
+
+// A ROWS-row operand tile (128-byte rows) fetched straight into LDS with
+// global_load_lds_dwordx4.  Each of the 4 waves issues NI = ROWS / 32 instructions per
+// stage; instruction i of wave wv fills the 1 KB LDS block wv * NI + i, i.e. rows
+// 8 (wv * NI + i) .. +8.  Lane l writes the block's 16-byte slot l, which is physical
+// chunk l % 8 of row 8 (wv * NI + i) + l / 8; the lane therefore fetches the logical
+// chunk (l % 8) ^ swz(row), so the tile lands in the swizzled lds_off layout.  Rows at or
+// past rmax re-read row rmax - 1 (their results are discarded by the caller).
+template <int ROWS>
+struct DmaTile {
+  static constexpr int NI = ROWS / 32;
+  uint32_t off[NI];  // per-lane byte offsets from the tile's first row, stage 0
+  // ld_bytes: row pitch in bytes; r0: first row; rmax: rows in the matrix
+  __device__ __forceinline__ void init(int64_t ld_bytes, int64_t r0, int64_t rmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = (wv * NI + i) * 8 + (lane >> 3);
+      int64_t r = r0 + row;
+      r = r < rmax ? r : rmax - 1;
+      const int chunk = (lane & 7) ^ swz(row);
+      off[i] = (uint32_t)((r - r0) * ld_bytes + chunk * 16);
+    }
+  }
+  // instruction i of one stage: `base` = the tile's first row at this stage's K offset,
+  // `dst` = the operand's LDS stage buffer (wave-uniform)
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
+                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * NI + i) * 1024),
+                                     16, 0, 0);
+  }
+};
+
+// Wait for this wave's LDS fills and all outstanding memory operations, then a
+// workgroup barrier.  The empty asm statements keep the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void fill_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Workgroup -> (tile t, split s) map for a persistent grid of TT x S workgroups.
+// Workgroups are dispatched round-robin over the 8 XCDs, and the C = G / 8 workgroups of
+// one XCD share its L2.  With xa > 0 each XCD holds a block of xa t-tiles x (C / xa)
+// splits, so one K stage of the block reads xa + C / xa distinct operand tiles through
+// that L2 (12 for a 4 x 8 block, against 18 for 16 x 2).  xa = 0: consecutive ids per
+// XCD, t fastest.
+__device__ __forceinline__ void wg_coords(int g, int G, int TT, int xa, int& t, int& s) {
+  if (xa > 0) {
+    const int C = G / kNumXcd, xb = C / xa;
+    const int x = g % kNumXcd, r = g / kNumXcd;
+    const int groups_t = TT / xa;
+    t = (x % groups_t) * xa + r % xa;
+    s = (x / groups_t) * xb + r / xa;
+    return;
+  }
+  int L = g;
+  if (G % kNumXcd == 0) L = (g % kNumXcd) * (G / kNumXcd) + g / kNumXcd;
+  s = L / TT;
+  t = L % TT;
+}
+
+// t-tiles per XCD block for a tt x splits grid (wg_coords): a divisor a of C = grid / 8
+// with tt % a == 0 and splits % (C / a) == 0, minimising a + C / a (distinct operand
+// tiles per K stage in one L2); 0 when no such block exists.
+inline int xcd_block(int tt, int splits) {
+  const int grid = tt * splits;
+  if (grid % kNumXcd) return 0;
+  const int C = grid / kNumXcd;
+  int best = 0;
+  for (int a = 1; a <= C; ++a) {
+    if (C % a || tt % a || splits % (C / a)) continue;
+    if (best == 0 || a + C / a < best + C / best) best = a;
+  }
+  return best;
+}
+
+}  // namespace ns
