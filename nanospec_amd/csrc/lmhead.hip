@@ -601,31 +601,6 @@ constexpr int kHeadLdsBytes = kLabelOff + 256 * 8;
 static_assert(kHeadLdsBytes <= 160 * 1024, "head kernel LDS");
 static_assert(kGemmLds <= kDumpLds, "the dump region covers the GEMM stages");
 
-// Eight values loaded as raw vectors, unpacked to fp32 later: keeping the unpack away from
-// the load lets all of a row group's loads be in flight together.
-template <typename T>
-struct Raw8;
-template <>
-struct Raw8<uint16_t> {
-  uint4 v;
-  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint4*>(p); }
-  __device__ __forceinline__ void unpack(float* f) const {
-    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
-  }
-};
-template <>
-struct Raw8<float> {
-  float4 a, b;
-  __device__ __forceinline__ void load(const float* p) {
-    a = reinterpret_cast<const float4*>(p)[0];
-    b = reinterpret_cast<const float4*>(p)[1];
-  }
-  __device__ __forceinline__ void unpack(float* f) const {
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-  }
-};
-
 // Butterfly partner within groups of 8 lanes, by DPP: step 0 swaps lanes 2i <-> 2i+1
 // (quad_perm [1,0,3,2]), step 1 swaps i <-> i^2 inside a quad (quad_perm [2,3,0,1]),
 // step 2 mirrors the 8 lanes (row_half_mirror: i <-> 7-i).  After steps 0 and 1 every

@@ -59,6 +59,46 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* f) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// Eight values loaded as raw vectors, unpacked to fp32 later: keeping the unpack away from
+// the load lets all of a row group's loads be in flight together.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<uint16_t> {
+  uint4 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void unpack(float* f) const {
+    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+  }
+};
+template <>
+struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void unpack(float* f) const {
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  }
+};
+
+// Non-temporal variant: a streamed output that nothing reads back soon.
+__device__ __forceinline__ void store8_nt(uint16_t* p, const float* f) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  const u32x4v v = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7])};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4v*>(p));
+}
+
+__device__ __forceinline__ void store8_nt(float* p, const float* f) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  const f32x4v a = {f[0], f[1], f[2], f[3]}, b = {f[4], f[5], f[6], f[7]};
+  __builtin_nontemporal_store(a, reinterpret_cast<f32x4v*>(p));
+  __builtin_nontemporal_store(b, reinterpret_cast<f32x4v*>(p) + 1);
+}
+
 __device__ __forceinline__ void store8(float* p, const float* f) {
   reinterpret_cast<float4*>(p)[0] = make_float4(f[0], f[1], f[2], f[3]);
   reinterpret_cast<float4*>(p)[1] = make_float4(f[4], f[5], f[6], f[7]);

@@ -13,8 +13,17 @@
 //   finalize          one workgroup: accept rate per row, block prefix
 //                     lengths, the six LossMetrics scalars (fixed order).
 // Every reduction has a fixed order, so results are bitwise reproducible.
+#include <type_traits>
+
 #include "ns_internal.h"
 #include "ns_profile.h"
+
+#ifndef NS_EMIT_UNROLL
+#define NS_EMIT_UNROLL 1
+#endif
+#ifndef NS_EMIT_NT
+#define NS_EMIT_NT 1
+#endif
 
 namespace ns {
 
@@ -191,27 +200,52 @@ __global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
   int64_t scalar_from = lo;
   if (VEC && lo < hi) {
     const int64_t nvec = (hi - lo) >> 3;
-    for (int64_t j = threadIdx.x; j < nvec; j += kStreamThreads) {
-      const int64_t i0 = lo + j * 8;
-      float zf[8], uf[8], d[8];
-      load8(zr + i0, zf);
-      load8(ur + i0, uf);
+    // U groups of 8 per iteration: all 2U loads are issued before any is used
+    auto body = [&](auto uc, int64_t j) {
+      constexpr int U = decltype(uc)::value;
+      Raw8<TZ> zraw[U];
+      Raw8<TU> uraw[U];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = fast_exp2(__builtin_fmaf(zf[e], kLog2e, -lzl));
-        const float t = fast_exp2(__builtin_fmaf(uf[e], kLog2e, -lul));
-        if (ACCEPT) acc += fminf(p, t);
-        if (EMIT) d[e] = __builtin_fmaf(cp, p, -ct * t);
+      for (int q = 0; q < U; ++q) {
+        zraw[q].load(zr + lo + (j + q * kStreamThreads) * 8);
+        uraw[q].load(ur + lo + (j + q * kStreamThreads) * 8);
       }
-      if (EMIT) {
-        if ((uint64_t)(y - i0) < 8ull) {
+      float zf[U][8], uf[U][8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (i0 + e == y) d[e] -= cy;
+      for (int q = 0; q < U; ++q) {
+        zraw[q].unpack(zf[q]);
+        uraw[q].unpack(uf[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < U; ++q) {
+        const int64_t i0 = lo + (j + q * kStreamThreads) * 8;
+        float d[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = fast_exp2(__builtin_fmaf(zf[q][e], kLog2e, -lzl));
+          const float t = fast_exp2(__builtin_fmaf(uf[q][e], kLog2e, -lul));
+          if (ACCEPT) acc += fminf(p, t);
+          if (EMIT) d[e] = __builtin_fmaf(cp, p, -ct * t);
         }
-        store8(dr + i0, d);
+        if (EMIT) {
+          if ((uint64_t)(y - i0) < 8ull) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (i0 + e == y) d[e] -= cy;
+          }
+#if NS_EMIT_NT
+          store8_nt(dr + i0, d);
+#else
+          store8(dr + i0, d);
+#endif
+        }
       }
-    }
+    };
+    int64_t j = threadIdx.x;
+#if NS_EMIT_UNROLL
+    for (; j + kStreamThreads < nvec; j += 2 * kStreamThreads) body(std::integral_constant<int, 2>{}, j);
+#endif
+    for (; j < nvec; j += kStreamThreads) body(std::integral_constant<int, 1>{}, j);
     scalar_from = lo + nvec * 8;
   }
   for (int64_t i = scalar_from + threadIdx.x; i < hi; i += kStreamThreads) {
