@@ -72,6 +72,7 @@ KERNEL_NAMES = [
     (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), false", "stream_accept"),
     (r"merge_kernel", "merge_rows"),
     (r"finalize_kernel", "finalize_metrics"),
+    (r"accept_rows_kernel", "accept_rows"),
     (r"fp8_quant_kernel", "fp8_quant"),
     (r"fp8_head_kernel", "fp8_head_gemm"),
     (r"prepare_kernel", "prepare_slots"),
@@ -235,8 +236,20 @@ def workload_c1(device, args):
     config = {"workload": "C1 logits-only: CE+KL+accept fwd + dlogits bwd over given bf16 [N,V] logits",
               "N": n, "V": v, "K": 8, "gamma": 4.0, "masked_rows": int((~slots.valid).sum()),
               "global_batch": n, "parallelism": "single GPU"}
+    def ceilings():
+        # library kernels with the same HBM access mix on the same tensors: two 2 GB
+        # reads (stream_stats) and two reads plus one write (stream_emit)
+        out = torch.empty_like(z)
+        read2 = _time_ms(lambda: (torch.sum(z), torch.sum(u)))
+        rw = _time_ms(lambda: torch.add(z, u, out=out))
+        del out
+        b = z.numel() * z.element_size()
+        return {"method": "torch.sum(z), torch.sum(u) and torch.add(z, u, out=) on the C1 tensors",
+                "read2_ms": read2, "read2_GBs": 2 * b / (read2 / 1e3) / 1e9,
+                "read2_write1_ms": rw, "read2_write1_GBs": 3 * b / (rw / 1e3) / 1e9}
+
     return dict(step=step, n=n, per_slot_bytes=per_slot, per_slot_flops=None, kernel_bytes=kernel_bytes,
-                kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16")
+                kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16", ceilings=ceilings)
 
 
 # --------------------------------------------------------------------------- C2 / C3
@@ -319,9 +332,18 @@ def workload_head(device, args, which):
     config = {"workload": f"{name}: LM-head GEMM + Markov addend + CE+KL+accept fwd, dl + dhidden bwd",
               "N": n, "d": d, "V": v, "K": 8, "gamma": gamma, "global_batch": n, "seq_len": None,
               "parallelism": "single GPU"}
+    def ceilings():
+        # the vendor library's plain GEMM of the same shape (hipBLASLt through torch.mm):
+        # the logits GEMM without any objective work, output written to HBM
+        ht = hidden.t().contiguous()   # a contiguous right operand (no transposed view)
+        mm = _time_ms(lambda: torch.mm(weight, ht))
+        del ht
+        return {"method": "torch.mm(W_lm, hidden^T) (hipBLASLt), bf16, random operands", "gemm_ms": mm,
+                "gemm_TFLOPs": gemm / (mm / 1e3) / 1e12}
+
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d, kernel_bytes=kernel_bytes,
                 kernel_flops=kernel_flops, kernel_fp8_flops=kernel_fp8_flops, cpu_baseline=cpu_baseline,
-                config=config, dtype="bf16" if fp8 is None else "bf16+fp8",
+                config=config, dtype="bf16" if fp8 is None else "bf16+fp8", ceilings=ceilings,
                 per_slot_fp8_flops=2.0 * v * d if fp8 is not None else None)
 
 
@@ -331,6 +353,21 @@ WORKLOADS = {
     "c3": lambda dev, a: workload_head(dev, a, "c3"),
     "c4": lambda dev, a: workload_head(dev, a, "c4"),
 }
+
+
+def _time_ms(fn, reps: int = 5) -> float:
+    """Mean time of fn() on the current stream (one untimed call first)."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def pmc_driver(step, device):
@@ -443,6 +480,9 @@ def main():
             ideal_s += wl["per_slot_fp8_flops"] * n / (FP8_PEAK_TFLOPS * 1e12)
         step_roof["mfma_frac"] = ideal_s / (ms_per_step / 1e3)
 
+    # practical ceilings measured with library kernels in this run (context for roofline)
+    ceil = wl["ceilings"]() if "ceilings" in wl else None
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = wl["cpu_baseline"](args.cpu_rows)
@@ -465,6 +505,7 @@ def main():
         "step_roofline": step_roof,
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "library_ceilings": ceil,
         "wall_s": wall,
         "host": {"cpu_model": cpu_model(), "cpu_count": os.cpu_count()},
         "device": torch.cuda.get_device_name(device),

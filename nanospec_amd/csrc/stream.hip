@@ -28,16 +28,28 @@
 namespace ns {
 
 constexpr int kStreamThreads = 256;
-constexpr int64_t kElemsPerBlock = 16384;   // target vocab elements per workgroup
-constexpr int kMaxSplits = 64;
+// Vocab entries per workgroup.  Pass 1 (read-only) is fastest with long ranges: few
+// partials and one block reduction per 16K entries.  Pass 2 reads two streams and writes
+// one; it moves bytes fastest with one 16-byte vector per thread and many short
+// workgroups (2048 entries), measured on MI355X: 6.3 TB/s against 5.1 TB/s at 16K.
+constexpr int64_t kStatsElems = 16384;
+constexpr int kStatsMaxSplits = 64;
+constexpr int64_t kEmitElems = 2048;
+constexpr int kEmitMaxSplits = 256;
+
+static int splits_for(int64_t v, int64_t elems, int max_splits) {
+  int64_t s = (v + elems - 1) / elems;
+  if (s < 1) s = 1;
+  if (s > max_splits) s = max_splits;
+  return (int)s;
+}
 
 int stream_splits(int64_t n, int64_t v) {
   (void)n;
-  int64_t s = (v + kElemsPerBlock - 1) / kElemsPerBlock;
-  if (s < 1) s = 1;
-  if (s > kMaxSplits) s = kMaxSplits;
-  return (int)s;
+  return splits_for(v, kStatsElems, kStatsMaxSplits);
 }
+
+static int emit_splits(int64_t v) { return splits_for(v, kEmitElems, kEmitMaxSplits); }
 
 static inline int64_t split_chunk(int64_t v, int splits) {
   const int64_t c = (v + splits - 1) / splits;
@@ -53,7 +65,7 @@ struct StreamWs {
 static size_t stream_ws_layout(int64_t n, int64_t v, void* base, StreamWs* out) {
   const int S = stream_splits(n, v);
   const size_t b1 = align_up((size_t)n * S * sizeof(RowPart), 256);
-  const size_t b2 = align_up((size_t)n * S * sizeof(float), 256);
+  const size_t b2 = align_up((size_t)n * emit_splits(v) * sizeof(float), 256);
   const size_t b3 = align_up((size_t)n * sizeof(float), 256);
   if (out) {
     char* p = static_cast<char*>(base);
@@ -264,6 +276,29 @@ __global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
   }
 }
 
+// ---------------------------------------------------------------- accept rate per row
+
+// One wave per row: lane l sums the row's pass-2 partials l, l + 64, ... in order, then
+// a butterfly sum (symmetric, so the result does not depend on the lane) -> row_stats.
+__global__ __launch_bounds__(256) void accept_rows_kernel(const float* __restrict__ parta, int splits, int64_t n,
+                                                          float* __restrict__ row_stats) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= n) return;
+  const int lane = threadIdx.x & 63;
+  const float* p = parta + r * splits;
+  float a = 0.f;
+  for (int s = lane; s < splits; s += 64) a += p[s];
+  a = wave_sum(a);
+  if (lane == 0) row_stats[r * kRowStatWidth + kAccept] = a;
+}
+
+static hipError_t launch_accept_rows(const float* parta, int splits, int64_t n, float* row_stats, hipStream_t st) {
+  NS_TIMED("accept_rows", st);
+  hipLaunchKernelGGL(accept_rows_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, parta, splits, n,
+                     row_stats);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- finalize
 
 constexpr int kFinalThreads = 1024;
@@ -395,12 +430,14 @@ static hipError_t forward_typed(const void* z, int64_t ldz, const void* u, int64
   hipError_t e = stats_dispatch<TZ, TU>(z, ldz, u, ldu, v, a, w, S, st);
   if (e != hipSuccess) return e;
   if ((e = launch_merge(w.part1, w.zy, v, S, a, row_stats, st)) != hipSuccess) return e;
+  const int S2 = emit_splits(v);
   if (dl != nullptr)
-    e = emit_dispatch<TZ, TU, true, true>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, w.parta, S, st);
+    e = emit_dispatch<TZ, TU, true, true>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, w.parta, S2, st);
   else
-    e = emit_dispatch<TZ, TU, false, true>(z, ldz, u, ldu, v, a, row_stats, nullptr, 0, w.parta, S, st);
+    e = emit_dispatch<TZ, TU, false, true>(z, ldz, u, ldu, v, a, row_stats, nullptr, 0, w.parta, S2, st);
   if (e != hipSuccess) return e;
-  return launch_finalize(w.parta, S, a, row_stats, metrics, st);
+  if ((e = launch_accept_rows(w.parta, S2, a.n, row_stats, st)) != hipSuccess) return e;
+  return launch_finalize(nullptr, 1, a, row_stats, metrics, st);   // accept rates already in row_stats
 }
 
 hipError_t stream_forward(const void* z, int zdt, int64_t ldz, const void* u, int udt, int64_t ldu,
@@ -420,7 +457,7 @@ hipError_t stream_backward(const void* z, int zdt, int64_t ldz, const void* u, i
                            int64_t v, const SlotArgs& a, const float* row_stats, void* dl, int64_t ldd,
                            hipStream_t st) {
   if (a.n == 0) return hipSuccess;
-  const int S = stream_splits(a.n, v);
+  const int S = emit_splits(v);
   if (zdt == kBF16 && udt == kBF16)
     return emit_dispatch<uint16_t, uint16_t, true, false>(z, ldz, u, ldu, v, a, row_stats, dl, ldd, nullptr, S, st);
   if (zdt == kBF16 && udt == kF32)
