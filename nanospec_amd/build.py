@@ -42,9 +42,17 @@ def flags() -> list[str]:
     ]
 
 
+# Per-file code-generation options.  fp8.hip: keep MFMA results (the per-128-K partial
+# products that VALU FMAs fold into the accumulator) in VGPRs; with them in AGPRs every
+# FMA needed a v_accvgpr_read first, which made the fp8 GEMM VALU-bound.
+FILE_FLAGS = {
+    "fp8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *flags(), "-c", src, "-o", obj]
+    cmd = [hipcc(), *flags(), *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stdout}\n{proc.stderr}")
