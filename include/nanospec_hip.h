@@ -8,6 +8,8 @@
  *   nanospec/ops.py:34-35 via train.py:272-279, 291   linear + ce_kl_loss fused
  *                                                     -> ns_lmhead_ce_kl_fwd
  *   nanospec/train.py:302         dh = dl @ lm_head.w -> ns_lmhead_bwd
+ *   nanospec/train.py:276-279 (MarkovHead, layers.py:74-78: embedding + linear)
+ *     fused into the LM head as a second K segment -> ns_lmhead_markov_ce_kl_fwd
  *
  * Conventions
  *   - All tensor arguments are device pointers; rows are `ld` elements apart,
@@ -35,7 +37,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 1
+#define NS_ABI_VERSION 2
 
 #define NS_BF16 0
 #define NS_F32 1
@@ -93,6 +95,19 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
                         const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
                         float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
                         float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+
+/* The same forward with the Markov head in factored form (train.py:276-279):
+ * z = hidden . weight^T + w1[prev] . w2^T, formed as one GEMM with K = d + r
+ * ([hidden | w1[prev]] . [weight | w2]^T), so no [N, V] Markov tensor is read.
+ * prev int64 [N]; w1 (markov_w1, nn.Embedding [V, r]) and w2 (markov_w2, nn.Linear
+ * [V, r]) bf16 with r % 64 == 0.  A prev id outside [0, V) makes its row's logits
+ * NaN (the reference's embedding lookup raises). */
+int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const int64_t* prev,
+                               const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r,
+                               const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
+                               const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
+                               float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
+                               float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream);
 
 /* LM-head backward dh = dl . weight (train.py:302): dl [N, V] bf16, weight [V, d]
  * bf16, dh [N, d] bf16.  Split-K over V with a fixed-order fp32 reduction. */

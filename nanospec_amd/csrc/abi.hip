@@ -117,11 +117,17 @@ int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, 
                     "ns_ce_kl_logits_bwd");
 }
 
-int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
-                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
-                        const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
-                        float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
-                        float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// Shared validation and launch of the fused forward (dense Markov addend or factors).
+int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                       int64_t ldm, const ns::MarkovFactors* factors, const void* teacher, int t_dtype, int64_t ldt,
+                       const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n, int64_t d,
+                       int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd,
+                       float* row_stats, float* metrics, void* workspace, size_t workspace_bytes,
+                       ns_stream_t stream, const char* name) {
   if (!dtype_ok(t_dtype)) return fail(NS_EDTYPE, "unsupported teacher dtype code %d", t_dtype);
   if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
   if (d < 64 || d % 64) return fail(NS_EINVAL, "hidden size must be a positive multiple of 64 (got %lld)", (long long)d);
@@ -137,14 +143,52 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
   if (!aligned(hidden) || !aligned(weight) || !aligned(teacher) || (markov && !aligned(markov)) || (dl && !aligned(dl)) ||
       ldh % 8 || ldw % 8 || (markov && ldm % 8) || ldt % tq || (dl && ldd % 8))
     return fail(NS_EALIGN, "fused head needs 16-byte aligned base pointers and rows");
+  if (factors) {
+    const int64_t r = factors->r;
+    if (r < 64 || r % 64) return fail(NS_EINVAL, "Markov rank must be a positive multiple of 64 (got %lld)", (long long)r);
+    if (n > 0 && !factors->prev) return fail(NS_ENULL, "prev is NULL");
+    if ((rc = check_matrix(factors->w1, v, r, factors->ldw1, "w1"))) return rc;
+    if ((rc = check_matrix(factors->w2, v, r, factors->ldw2, "w2"))) return rc;
+    if (!aligned(factors->w1) || !aligned(factors->w2) || factors->ldw1 % 8 || factors->ldw2 % 8)
+      return fail(NS_EALIGN, "Markov factors need 16-byte aligned base pointers and rows");
+    // gathered W1 rows are addressed with 32-bit byte offsets from its base
+    if (v * factors->ldw1 * 2 >= (int64_t(1) << 32))
+      return fail(NS_EINVAL, "w1 spans %lld bytes; at most 4 GiB", (long long)(v * factors->ldw1 * 2));
+  }
   const size_t need = ns::lmhead_workspace_bytes(n, v, d);
   if (n > 0 && (!workspace || workspace_bytes < need))
     return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
   ns::SlotArgs a{labels, weights, valid, n, k, c_ce, c_kl, inv_acc};
-  return hip_status(ns::lmhead_forward(hidden, ldh, weight, ldw, markov, ldm, teacher, t_dtype, ldt, d, v, a, dl, ldd,
-                                       row_stats, metrics, workspace, reinterpret_cast<hipStream_t>(stream)),
-                    "ns_lmhead_ce_kl_fwd");
+  return hip_status(ns::lmhead_forward(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, d, v,
+                                       a, dl, ldd, row_stats, metrics, workspace, reinterpret_cast<hipStream_t>(stream)),
+                    name);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
+                        const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
+                        float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
+                        float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+  return lmhead_fwd_checked(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, labels, weights,
+                            valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, workspace,
+                            workspace_bytes, stream, "ns_lmhead_ce_kl_fwd");
+}
+
+int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const int64_t* prev,
+                               const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r,
+                               const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
+                               const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
+                               float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
+                               float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+  const ns::MarkovFactors f{prev, w1, w2, ldw1, ldw2, r};
+  return lmhead_fwd_checked(hidden, ldh, weight, ldw, nullptr, 0, &f, teacher, t_dtype, ldt, labels, weights, valid,
+                            n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, workspace, workspace_bytes,
+                            stream, "ns_lmhead_markov_ce_kl_fwd");
 }
 
 int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,

@@ -265,16 +265,13 @@ __device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la
 //           everyone), then fragment reads of stage t + 1 step 0 and the A fills of
 //           stage t + 2 into buffer t & 1.
 // Fills past the last stage re-read the last stage into the idle buffer.
-__device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
-                                        int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
-                                        int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
-  const int KT = (int)(K / BK);
+//
+// The operand tiles come in ready-made: `ta`/`tb` hold the per-lane offsets of the
+// 256 rows of each operand from the uniform bases `pa`/`pb` (stage 0), and stage t reads
+// 128 bytes further along K each step; KT stages.
+__device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTile<256>& ta, const char* pa,
+                                              const DmaTile<256>& tb, const char* pb, int KT, lds_t* lds) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  DmaTile<256> ta, tb;
-  ta.init(lda * 2, a0, amax, wv);
-  tb.init(ldb * 2, b0, bmax, wv);
-  const char* pa = reinterpret_cast<const char*>(A + a0 * lda);
-  const char* pb = reinterpret_cast<const char*>(B + b0 * ldb);
   auto stage_k = [&](int t) -> int64_t { return (int64_t)(t < KT - 1 ? t : KT - 1) * BK * 2; };
   auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * 2 * kStageBytes; };
 #pragma unroll
@@ -332,6 +329,19 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
     }
   }
   fill_barrier();
+}
+
+// acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T (row-major, K contiguous, K % BK == 0);
+// rows at or past amax / bmax re-read the last row.
+__device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
+                                        int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
+                                        int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  DmaTile<256> ta, tb;
+  ta.init(lda * 2, a0, amax, wv);
+  tb.init(ldb * 2, b0, bmax, wv);
+  gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(A + a0 * lda), tb, reinterpret_cast<const char*>(B + b0 * ldb),
+                (int)(K / BK), lds);
 }
 
 // B operand [K rows, cols] (cols contiguous) fetched straight into a row-major LDS
@@ -577,6 +587,11 @@ struct HeadParams {
   int64_t n, d, v;
   int tt, vt, splits;       // token tiles, vocab tiles, vocab splits
   int xa;                   // token tiles per XCD block (wg_coords), 0 = unblocked
+  // Markov head as a second K segment (r > 0): z += W1[prev] . W2^T
+  const int64_t* prev;      // [N] previous-token ids
+  const uint16_t* w1;       // [V, r] bf16 (embedding)
+  const uint16_t* w2;       // [V, r] bf16 (projection)
+  int64_t ldw1, ldw2, r;
   const int64_t* labels;
   const float* weights;
   float c_ce, c_kl, inv_acc;
@@ -597,7 +612,9 @@ enum { MODE_STATS = 0, MODE_EMIT = 1, MODE_STORE = 2 };
 constexpr int kStateOff = kDumpLds;                   // [256][8] fp32: mz sz mu su A | arate
 constexpr int kConstOff = kStateOff + 256 * 8 * 4;    // [256][8] fp32: lzl lul cp ct cy
 constexpr int kLabelOff = kConstOff + 256 * 8 * 4;    // [256] int64 labels
-constexpr int kHeadLdsBytes = kLabelOff + 256 * 8;
+constexpr int kPrevOff = kLabelOff + 256 * 8;        // [256] int32 W1 rows (ids clamped to [0, V))
+constexpr int kBadOff = kPrevOff + 256 * 4;          // [256] uint8: id outside [0, V)
+constexpr int kHeadLdsBytes = kBadOff + 256;
 static_assert(kHeadLdsBytes <= 160 * 1024, "head kernel LDS");
 static_assert(kGemmLds <= kDumpLds, "the dump region covers the GEMM stages");
 
@@ -688,10 +705,17 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
 #pragma unroll
       for (int e = 0; e < 4; ++e) { z[8 * k + e] = x0[e]; z[8 * k + 4 + e] = x1[e]; }
     }
+    // a previous-token id outside [0, V) has no Markov row: its logits become NaN, so the
+    // loss reports the bad input (the reference's embedding lookup raises)
+    const bool bad = p.r > 0 && reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tk];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       float mk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (has_m) mraw[k].unpack(mk);
+      if (bad) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mk[e] = __builtin_nanf("");
+      }
       if (MODE != MODE_STORE) uraw[k].unpack(u + 8 * k);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -766,6 +790,13 @@ void head_kernel(HeadParams p) {
 
   // per-token state and constants of this workgroup's 256 tokens (thread tid: token tid);
   // first read after the GEMM's barriers
+  if (p.r > 0) {
+    const int64_t t = t0 + tid;
+    const int64_t id = p.prev[t < p.n ? t : p.n - 1];
+    const bool ok = id >= 0 && id < p.v;
+    reinterpret_cast<__attribute__((address_space(3))) int*>(lds + kPrevOff)[tid] = ok ? (int)id : 0;
+    reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tid] = ok ? 0 : 1;
+  }
   if (MODE != MODE_STORE) {
     const int64_t t = t0 + tid;
     const int64_t trow = t < p.n ? t : p.n - 1;
@@ -790,6 +821,14 @@ void head_kernel(HeadParams p) {
     const int64_t v0 = (int64_t)vt * BM;
     zero_acc(acc);
     gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds);
+    if (p.r > 0) {   // Markov K segment: W2[v-tile] . W1[prev[t-tile]]^T
+      const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+      DmaTile<256> ta, tb;
+      ta.init(p.ldw2 * 2, v0, p.v, wv);
+      tb.init_gather(p.ldw1 * 2, reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kPrevOff), wv);
+      gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.w2 + v0 * p.ldw2), tb,
+                    reinterpret_cast<const char*>(p.w1), (int)(p.r / BK), lds);
+    }
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       if (wn == jj) dump_half(acc, lds);
@@ -1020,9 +1059,9 @@ size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d) {
 }
 
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
-                          int64_t ldm, const void* teacher, int tdt, int64_t ldt, int64_t d, int64_t v,
-                          const SlotArgs& a, void* dl, int64_t ldd, float* row_stats, float* metrics, void* ws,
-                          hipStream_t st) {
+                          int64_t ldm, const MarkovFactors* factors, const void* teacher, int tdt, int64_t ldt,
+                          int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd, float* row_stats,
+                          float* metrics, void* ws, hipStream_t st) {
   if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
   const HeadPlan pl = head_plan(a.n, v);
   HeadWs w;
@@ -1039,6 +1078,12 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
   p.c_ce = a.c_ce; p.c_kl = a.c_kl; p.inv_acc = a.inv_acc;
   p.part1 = w.part1; p.zy = w.zy; p.parta = w.parta;
   p.dl = static_cast<uint16_t*>(dl); p.ldd = ldd;
+  if (factors) {
+    p.prev = factors->prev;
+    p.w1 = static_cast<const uint16_t*>(factors->w1);
+    p.w2 = static_cast<const uint16_t*>(factors->w2);
+    p.ldw1 = factors->ldw1; p.ldw2 = factors->ldw2; p.r = factors->r;
+  }
   if (tdt == kBF16) return head_forward_typed<uint16_t>(p, pl, a, row_stats, metrics, w, st);
   return head_forward_typed<float>(p, pl, a, row_stats, metrics, w, st);
 }

@@ -46,6 +46,18 @@ struct DmaTile {
       off[i] = (uint32_t)((r - r0) * ld_bytes + chunk * 16);
     }
   }
+  // Gathered rows: tile row j is matrix row rows[j] (rows[] in LDS, already in range),
+  // offsets from the matrix base.
+  __device__ __forceinline__ void init_gather(int64_t ld_bytes, const __attribute__((address_space(3))) int* rows,
+                                              int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = (wv * NI + i) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ swz(row);
+      off[i] = (uint32_t)((int64_t)rows[row] * ld_bytes + chunk * 16);
+    }
+  }
   // instruction i of one stage: `base` = the tile's first row at this stage's K offset,
   // `dst` = the operand's LDS stage buffer (wave-uniform)
   __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {

@@ -39,10 +39,17 @@ hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, fl
                            float* metrics, hipStream_t st);
 
 // ---- fused LM-head path (lmhead.hip) ---------------------------------------
+// Markov head in factored form: logits += W1[prev] . W2^T (rank r, r % 64 == 0).
+struct MarkovFactors {
+  const int64_t* prev;   // [N] previous-token ids
+  const void* w1;        // [V, r] bf16, row stride ldw1
+  const void* w2;        // [V, r] bf16, row stride ldw2
+  int64_t ldw1, ldw2, r;
+};
 size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d);
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
-                          const void* markov, int64_t ldm, const void* teacher, int tdt, int64_t ldt,
-                          int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd,
+                          const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
+                          int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd,
                           float* row_stats, float* metrics, void* ws, hipStream_t st);
 size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d);
 hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh,

@@ -28,6 +28,17 @@ from nanospec_amd.objective import LossMetrics, _slot_inputs
 
 
 @dataclass
+class MarkovFactors:
+    """The Markov head in factored form (MarkovHead, layers.py:74-78; train.py:276-279):
+    logits += markov_w1[previous] . markov_w2^T.  previous int64 [..., K] (the
+    prepared batch's previous ids), w1 / w2 bf16 [V, r] with r % 64 == 0."""
+
+    previous: torch.Tensor
+    w1: torch.Tensor
+    w2: torch.Tensor
+
+
+@dataclass
 class HeadActivations:
     """State the fused backward needs: per-row statistics, the emitted dl and the
     frozen head weight.  row_stats [N, 8] = (lse_z, lse_u, ce, kl, accept_rate, z_label, 0, 0)."""
@@ -38,6 +49,7 @@ class HeadActivations:
     dlogits: torch.Tensor | None
     accumulation_steps: int
     shape: tuple
+    markov: MarkovFactors | None = None
 
 
 def _bf16_rows(t: torch.Tensor, cols: int, name: str):
@@ -48,13 +60,15 @@ def _bf16_rows(t: torch.Tensor, cols: int, name: str):
 
 @torch.no_grad()
 def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objective, *, markov_logits=None,
-                       accumulation_steps=1, emit_dlogits=True):
+                       markov=None, accumulation_steps=1, emit_dlogits=True):
     """Fused forward: LM-head projection (+ Markov addend) and the CE + KL + accept objective.
 
     hidden [..., K, d] bf16; lm_head_weight [V, d] bf16; target_logits [..., K, V]
     bf16 or fp32; markov_logits [..., K, V] bf16 or None; prepared has weights,
     target_ids, valid [..., K].  dl is emitted for ``accumulation_steps`` (pass the
-    same value to the backward).
+    same value to the backward).  ``markov`` (a ``MarkovFactors``) adds the Markov
+    head in factored form instead of a dense ``markov_logits`` tensor: it is fused
+    into the GEMM as a second K segment, and the backward can form its gradients.
     """
     o = objective
     if accumulation_steps < 1:
@@ -74,22 +88,42 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
             raise ValueError(f"markov_logits has {m.shape[0]} rows, hidden has {n}")
     else:
         m, ldm = None, vocab
+    if markov is not None and markov_logits is not None:
+        raise ValueError("pass either markov_logits or markov factors, not both")
     wts, y, valid, k = _slot_inputs(prepared, n, device)
     metrics = torch.empty(6, dtype=torch.float32, device=device)
     row_stats = torch.empty((n, 8), dtype=torch.float32, device=device)
     dl = torch.empty((n, vocab), dtype=torch.bfloat16, device=device) if emit_dlogits else None
     ws = _lib.workspace(_lib.NS_WS_LMHEAD, n, vocab, d, device)
-    status = lib.ns_lmhead_ce_kl_fwd(
-        _lib.ptr(h), ldh, _lib.ptr(w), ldw, _lib.ptr(m), ldm, _lib.ptr(u), _lib.dtype_code(u), ldu,
-        _lib.ptr(y), _lib.ptr(wts), _lib.ptr(valid), n, d, vocab, k,
-        float(o.ce), float(o.kl), 1.0 / accumulation_steps,
-        _lib.ptr(dl), vocab, _lib.ptr(row_stats), _lib.ptr(metrics),
-        _lib.ptr(ws), ws.numel(), _lib.stream(device),
-    )
-    _lib.check(status, "ns_lmhead_ce_kl_fwd")
+    tail = (_lib.ptr(u), _lib.dtype_code(u), ldu, _lib.ptr(y), _lib.ptr(wts), _lib.ptr(valid), n, d, vocab, k,
+            float(o.ce), float(o.kl), 1.0 / accumulation_steps, _lib.ptr(dl), vocab, _lib.ptr(row_stats),
+            _lib.ptr(metrics), _lib.ptr(ws), ws.numel(), _lib.stream(device))
+    if markov is None:
+        status = lib.ns_lmhead_ce_kl_fwd(_lib.ptr(h), ldh, _lib.ptr(w), ldw, _lib.ptr(m), ldm, *tail)
+        _lib.check(status, "ns_lmhead_ce_kl_fwd")
+    else:
+        prev, w1, ldw1, w2, ldw2, r = _markov_inputs(markov, vocab, n, device)
+        status = lib.ns_lmhead_markov_ce_kl_fwd(_lib.ptr(h), ldh, _lib.ptr(w), ldw, _lib.ptr(prev), _lib.ptr(w1),
+                                                ldw1, _lib.ptr(w2), ldw2, r, *tail)
+        _lib.check(status, "ns_lmhead_markov_ce_kl_fwd")
     shape = tuple(hidden.shape[:-1]) + (vocab,)
-    saved = HeadActivations(o, lm_head_weight, row_stats, dl, accumulation_steps, shape)
+    saved = HeadActivations(o, lm_head_weight, row_stats, dl, accumulation_steps, shape, markov)
     return LossMetrics.from_buffer(metrics), saved
+
+
+def _markov_inputs(markov: MarkovFactors, vocab: int, n: int, device):
+    """Flatten and check the factored Markov head's inputs."""
+    prev = markov.previous.reshape(-1).to(device=device, dtype=torch.int64).contiguous()
+    if prev.numel() != n:
+        raise ValueError(f"markov.previous has {prev.numel()} entries, hidden has {n} rows")
+    if markov.w1.dim() != 2 or markov.w2.dim() != 2 or markov.w1.shape != markov.w2.shape:
+        raise ValueError(f"markov w1 {tuple(markov.w1.shape)} and w2 {tuple(markov.w2.shape)} must both be [V, r]")
+    if markov.w1.shape[0] != vocab:
+        raise ValueError(f"markov weights have {markov.w1.shape[0]} rows, the vocabulary is {vocab}")
+    r = markov.w1.shape[1]
+    w1, ldw1 = _bf16_rows(markov.w1, r, "markov.w1")
+    w2, ldw2 = _bf16_rows(markov.w2, r, "markov.w2")
+    return prev, w1, ldw1, w2, ldw2, r
 
 
 @torch.no_grad()

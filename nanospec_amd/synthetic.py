@@ -83,6 +83,17 @@ def head_inputs(n, d, v, seed, device, *, ragged=False, gamma=4.0, k=BLOCK):
     return hidden, weight, markov, teacher, slots
 
 
+def markov_factors(n, v, r, seed, device):
+    """Factored Markov head (MarkovHead, layers.py:74-78): previous ids ~ U[0, V),
+    w1 ~ N(0, 1), w2 ~ N(0, 0.05) (bf16), so w1[prev] . w2^T has std about
+    0.05 sqrt(r) (0.8 at r = 256, like the dense recipe's N(0, 0.5))."""
+    g = _gen(seed, device)
+    prev = torch.randint(0, v, (n,), generator=g, device=device)
+    w1 = torch.randn((v, r), generator=g, device=device).to(torch.bfloat16)
+    w2 = (0.05 * torch.randn((v, r), generator=g, device=device)).to(torch.bfloat16)
+    return prev, w1, w2
+
+
 def c0(device="cpu"):
     """C0 CPU plumbing: N = 64 (8 x 8), d = 256, V = 8192, gamma 4, all valid."""
     return head_inputs(64, 256, 8192, 1000, device)

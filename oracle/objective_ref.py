@@ -22,6 +22,9 @@ ce_kl_loss                 torch library loss (cross_entropy + kl_div);
 ce_kl_backward             torch.autograd on the library loss; rows sum to 0;
                            w = 0 rows are 0; linear in 1/accumulation_steps
 lm_head_logits / dhidden   torch fp64 matmul; linearity
+markov_logits / backward   torch F.embedding + F.linear forward, torch.autograd
+                           for d(previous), d(w2) and the index_add d(w1);
+                           hand-worked index_add with repeated ids
 slot_preparation           hand-computed known answers; brute-force loops
 e4m3 round / fp8_linear    torch ``float8_e4m3fn`` cast; exact products for
                            e4m3-grid inputs with power-of-two scales
@@ -292,6 +295,30 @@ def lm_head_logits(hidden, weight, markov=None, dtype=np.float64):
 def lm_head_backward(dl, weight, dtype=np.float64):
     """dh = dl . W_lm  (train.py:302)."""
     return np.asarray(dl, dtype=dtype) @ np.asarray(weight, dtype=dtype)
+
+
+def markov_logits(prev, w1, w2, dtype=np.float64):
+    """Markov-head logits w1[prev] . w2^T (train.py:276-279: ops.embedding then
+    ops.linear, ops.py:69-70 and 34-35; MarkovHead layers.py:74-78).  The fp32
+    objective adds them to the LM-head logits unrounded."""
+    e = np.asarray(w1, dtype=dtype)[np.asarray(prev, dtype=np.int64)]
+    return e @ np.asarray(w2, dtype=dtype).T
+
+
+def markov_backward(dl, prev, w1, w2, dtype=np.float64):
+    """Gradients of the Markov head given dl (train.py:303-307):
+    d(previous) = dl . w2 (ops.linear_backward, ops.py:38-45), d(w2) = dl^T . w1[prev]
+    (copied into w2.grad), d(w1) = zeros.index_add(prev, d(previous))
+    (ops.embedding_backward, ops.py:73-74).  Returns (d_previous, d_w2, d_w1)."""
+    dl = np.asarray(dl, dtype=dtype)
+    w2 = np.asarray(w2, dtype=dtype)
+    prev = np.asarray(prev, dtype=np.int64)
+    e = np.asarray(w1, dtype=dtype)[prev]
+    dprev = dl @ w2
+    dw2 = dl.T @ e
+    dw1 = np.zeros(np.shape(w1), dtype=dtype)
+    np.add.at(dw1, prev, dprev)
+    return dprev, dw2, dw1
 
 
 # ---------------------------------------------------------------------------

@@ -195,6 +195,34 @@ def test_lm_head_matches_torch_matmul():
     np.testing.assert_allclose(ref.lm_head_backward(2 * dl, w), 2 * dh, rtol=1e-13)
 
 
+def test_markov_head_matches_torch_embedding_linear_and_autograd():
+    """Forward = F.linear(F.embedding(prev, w1), w2) (train.py:278-279); the three
+    gradients = torch.autograd of sum(dl * logits), which is what the reference's
+    handwritten linear_backward / embedding_backward compute (ops.py:38-45, 73-74)."""
+    g = np.random.default_rng(33)
+    n, v, r = 12, 40, 8
+    prev = g.integers(0, v, n)
+    prev[3] = prev[7] = prev[9] = 5            # repeated ids: index_add sums their rows
+    w1, w2, dl = g.standard_normal((v, r)), g.standard_normal((v, r)), g.standard_normal((n, v))
+    tw1 = torch.from_numpy(w1).requires_grad_()
+    tw2 = torch.from_numpy(w2).requires_grad_()
+    tprev = torch.from_numpy(prev)
+    e = F.embedding(tprev, tw1)
+    e.retain_grad()
+    logits = F.linear(e, tw2)
+    np.testing.assert_allclose(ref.markov_logits(prev, w1, w2), logits.detach().numpy(), rtol=1e-12, atol=1e-12)
+    (logits * torch.from_numpy(dl)).sum().backward()
+    dprev, dw2, dw1 = ref.markov_backward(dl, prev, w1, w2)
+    np.testing.assert_allclose(dprev, e.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dw2, tw2.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dw1, tw1.grad.numpy(), rtol=1e-12, atol=1e-12)
+    # hand-worked index_add: row 5 collects rows 3, 7 and 9 of d(previous) (plus any other 5s)
+    hits = np.flatnonzero(prev == 5)
+    np.testing.assert_allclose(dw1[5], dprev[hits].sum(axis=0), rtol=1e-12)
+    untouched = np.setdiff1d(np.arange(v), prev)
+    assert np.all(dw1[untouched] == 0)
+
+
 # --------------------------------------------------------------- formats / fp8
 
 
