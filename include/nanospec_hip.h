@@ -10,6 +10,7 @@
  *   nanospec/train.py:302         dh = dl @ lm_head.w -> ns_lmhead_bwd
  *   nanospec/train.py:276-279 (MarkovHead, layers.py:74-78: embedding + linear)
  *     fused into the LM head as a second K segment -> ns_lmhead_markov_ce_kl_fwd
+ *   nanospec/train.py:302-307     dh, markov_w2.grad, markov_w1.grad -> ns_lmhead_markov_bwd
  *
  * Conventions
  *   - All tensor arguments are device pointers; rows are `ld` elements apart,
@@ -113,6 +114,22 @@ int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weig
  * bf16, dh [N, d] bf16.  Split-K over V with a fixed-order fp32 reduction. */
 int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
                   int64_t n, int64_t v, int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+
+/* Scratch bytes ns_lmhead_markov_bwd needs for n slots, vocabulary v, hidden d, rank r. */
+size_t ns_lmhead_markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r);
+
+/* Head backward with the factored Markov head (train.py:302-307):
+ *   dh = dl . weight                                          (train.py:302)
+ *   w2_grad = dl^T . w1[prev]      overwritten, bf16 [V, r]  (ops.py:38-45, copy_)
+ *   w1_grad.index_add_(0, prev, dl . w2)   accumulated, bf16 (ops.py:73-74)
+ * d(previous) = dl . w2 comes out of the dh GEMM as extra column tiles (fp32, never
+ * rounded); each w1_grad row receives the fp32 sum of its tokens' rows, added in token
+ * order (deterministic), rounded once.  Rows whose prev id is outside [0, V) add
+ * nothing to w1_grad.  Requires V, d % 8 == 0, r % 64 == 0, n < 2^31. */
+int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const int64_t* prev,
+                         const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r, void* dh,
+                         int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2, int64_t n, int64_t v,
+                         int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream);
 
 /* Plain LM-head projection out = x . weight^T (+ addend), bf16 out (ops.py:34-35 for
  * the head: train.py:272, 279, 284).  x [N, d], weight [V, d], addend [N, V] or NULL. */

@@ -211,6 +211,42 @@ int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, 
                     "ns_lmhead_bwd");
 }
 
+size_t ns_lmhead_markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r) {
+  if (n < 0 || v < 0 || d < 0 || r < 0) return 0;
+  return ns::markov_bwd_workspace_bytes(n, v, d, r);
+}
+
+int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const int64_t* prev,
+                         const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r, void* dh,
+                         int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2, int64_t n, int64_t v,
+                         int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+  if (n < 0 || n >= (int64_t(1) << 31)) return fail(NS_EINVAL, "n must be in [0, 2^31) (got %lld)", (long long)n);
+  if (v < 8 || v % 8 || v >= (int64_t(1) << 31))
+    return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 below 2^31 (got %lld)", (long long)v);
+  if (d < 8 || d % 8) return fail(NS_EINVAL, "hidden size must be a positive multiple of 8 (got %lld)", (long long)d);
+  if (r < 64 || r % 64) return fail(NS_EINVAL, "Markov rank must be a positive multiple of 64 (got %lld)", (long long)r);
+  if (n > 0 && !prev) return fail(NS_ENULL, "prev is NULL");
+  int rc;
+  if ((rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
+  if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
+  if ((rc = check_matrix(w1, v, r, ldw1, "w1"))) return rc;
+  if ((rc = check_matrix(w2, v, r, ldw2, "w2"))) return rc;
+  if ((rc = check_matrix(dh, n, d, lddh, "dh"))) return rc;
+  if ((rc = check_matrix(w1_grad, v, r, ldg1, "w1_grad"))) return rc;
+  if ((rc = check_matrix(w2_grad, v, r, ldg2, "w2_grad"))) return rc;
+  if (!aligned(dl) || !aligned(weight) || !aligned(w1) || !aligned(w2) || !aligned(dh) || !aligned(w1_grad) ||
+      !aligned(w2_grad) || ldd % 8 || ldw % 8 || ldw1 % 8 || ldw2 % 8 || lddh % 4 || ldg1 % 8 || ldg2 % 8)
+    return fail(NS_EALIGN, "Markov backward needs 16-byte aligned base pointers and rows");
+  const size_t need = ns::markov_bwd_workspace_bytes(n, v, d, r);
+  if (n > 0 && (!workspace || workspace_bytes < need))
+    return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  const ns::MarkovFactors f{prev, w1, w2, ldw1, ldw2, r};
+  return hip_status(ns::markov_backward(dl, ldd, weight, ldw, f, dh, lddh, w1_grad, ldg1, w2_grad, ldg2, n, v, d,
+                                        workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_markov_bwd");
+}
+
 int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                      int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, ns_stream_t stream) {
   if (n < 0) return fail(NS_EINVAL, "n must be >= 0");

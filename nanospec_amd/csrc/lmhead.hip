@@ -344,62 +344,6 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
                 (int)(K / BK), lds);
 }
 
-// B operand [K rows, cols] (cols contiguous) fetched straight into a row-major LDS
-// stage: 64 K rows of 512 bytes, the 16-byte chunk cn of row k stored at physical
-// chunk cn ^ (4 (k & 3)), which keeps the transposed fragment reads (tr_b16) free of
-// bank conflicts.  Instruction i of wave wv fills rows 2 (wv * 8 + i) + {0, 1}; lane l
-// writes physical chunk l % 32 of row 2 (wv * 8 + i) + l / 32.  Column chunks at or
-// past cmax re-read the tile's first chunk (discarded by the caller).
-struct DmaTileKN {
-  uint32_t off[8];
-  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 2 * (wv * 8 + i) + (lane >> 5);
-      const int cn = (lane & 31) ^ (4 * (row & 3));
-      int64_t col = c0 + cn * 8;
-      col = col < cmax ? col : c0;
-      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
-    }
-  }
-  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
-                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * 8 + i) * 1024),
-                                     16, 0, 0);
-  }
-};
-
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-
-// B fragment i (32 columns) of step kk from a DmaTileKN stage, as two transposed reads:
-// ds_read_b64_tr_b16 gives lane 16 g + x of a 16-lane group element x % 4 of the
-// 8-byte pieces addressed by lanes 16 g + 4 j + x / 4, j = 0..3.  Lane 16 g + 4 j + m
-// addresses row kbase + j, columns nb + 4 m .. +3, so lane 16 g + x receives
-// B[kbase + 0..3][nb + x]: K-contiguous, as the MFMA B operand wants.
-struct TrFrag {
-  i16x4_t lo, hi;  // K 0..3 and 4..7 of this lane's eight
-};
-
-__device__ __forceinline__ uint32_t tr_base(int wn, int i) {
-  // byte address of this lane's piece for step 0, half 0 (add 2048 for half 1, 8192 per step)
-  const int lane = threadIdx.x & 63;
-  const int x = lane & 15;
-  const int row = 8 * (lane >> 5) + (x >> 2);                       // + 16 kk + 4 half
-  const int col = wn * 128 + i * 32 + 16 * ((lane >> 4) & 1) + 4 * (x & 3);
-  const int cn = (col >> 3) ^ (4 * (row & 3));
-  return (uint32_t)(row * 512 + (cn << 4) + (col & 7) * 2);
-}
-
-__device__ __forceinline__ i16x4_t tr_read(const lds_t* buf, uint32_t addr) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      reinterpret_cast<__attribute__((address_space(3))) i16x4_t*>(const_cast<lds_t*>(buf) + addr));
-}
-
-__device__ __forceinline__ bf16x8_t tr_join(const TrFrag& f) {
-  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(f.lo, f.hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
 // acc += A[a0:a0+256, k0:k0+64 KT] . B[k0:k0+64 KT, c0:c0+256] over KT full stages,
 // A row-major (K contiguous), B row-major [K, cols].  Both operands go global -> LDS
 // without registers, as in gemm_nt; B fragments use transposed LDS reads.  Per stage t:
@@ -865,6 +809,12 @@ struct BwdParams {
   int xa, xb;              // XCD block: xa token tiles x xb d tiles per round (0 = unblocked)
   int kt_total;            // ceil(V / BK)
   float* part;             // [ksplit][N][d] fp32
+  // Markov extension (r > 0): column tiles ct >= ct_main multiply by w2 [V, r]
+  // instead, into part2 [ksplit][N][r] (d(previous) = dl . w2)
+  const uint16_t* w2;
+  int64_t ldw2, r;
+  int ct_main;
+  float* part2;
 };
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -897,7 +847,12 @@ void dh_kernel(BwdParams p) {
   }
   const int kt0 = (int)((int64_t)ks * p.kt_total / p.ksplit);
   const int kt1 = (int)((int64_t)(ks + 1) * p.kt_total / p.ksplit);
-  const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)ct * BN;
+  // the column tile reads W_lm, or w2 for the Markov extension tiles
+  const bool mk = ct >= p.ct_main;
+  const uint16_t* B = mk ? p.w2 : p.weight;
+  const int64_t ldb = mk ? p.ldw2 : p.ldw;
+  const int64_t cols = mk ? p.r : p.d;
+  const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)(mk ? ct - p.ct_main : ct) * BN;
   f32x16_t acc[4][4];
   zero_acc(acc);
   // full stages straight into LDS; a partial last stage (V % BK != 0) through registers,
@@ -905,14 +860,13 @@ void dh_kernel(BwdParams p) {
   const int kfull = (int)(p.v / BK);
   const int kt_dma_end = kt1 < kfull ? kt1 : kfull;
   if (kt_dma_end > kt0)
-    gemm_nn_dma(acc, p.dl, p.ldd, m0, p.n, p.weight, p.ldw, c0, p.d, (int64_t)kt0 * BK, kt_dma_end - kt0, lds);
+    gemm_nn_dma(acc, p.dl, p.ldd, m0, p.n, B, ldb, c0, cols, (int64_t)kt0 * BK, kt_dma_end - kt0, lds);
   if (kt1 > kt_dma_end)
-    gemm_nn(acc, p.dl, p.ldd, m0, p.n, p.weight, p.ldw, c0, p.d, (int64_t)kt_dma_end * BK, (int64_t)kt1 * BK, p.v,
-            lds);
+    gemm_nn(acc, p.dl, p.ldd, m0, p.n, B, ldb, c0, cols, (int64_t)kt_dma_end * BK, (int64_t)kt1 * BK, p.v, lds);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int h = lane >> 5;
-  float* out = p.part + (int64_t)ks * p.n * p.d;
+  float* out = (mk ? p.part2 : p.part) + (int64_t)ks * p.n * cols;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -921,9 +875,24 @@ void dh_kernel(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
-        if (row < p.n && col < p.d) out[row * p.d + col] = acc[i][j][e];
+        if (row < p.n && col < cols) out[row * cols + col] = acc[i][j][e];
       }
     }
+}
+
+// fp32 sum of split partials [ksplit][N][d] into fp32 out [N][d] (row stride ldo), fixed order.
+__global__ __launch_bounds__(256) void sum_partials_kernel(const float* __restrict__ part, int ksplit, int64_t n,
+                                                           int64_t d, float* __restrict__ out, int64_t ldo) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int64_t total = n * d;
+  if (idx >= total) return;
+  const int64_t row = idx / d, col = idx % d;
+  float4 s = *reinterpret_cast<const float4*>(part + idx);
+  for (int k = 1; k < ksplit; ++k) {
+    const float4 x = *reinterpret_cast<const float4*>(part + (int64_t)k * total + idx);
+    s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+  }
+  *reinterpret_cast<float4*>(out + row * ldo + col) = s;
 }
 
 __global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict__ part, int ksplit, int64_t n,
@@ -996,13 +965,15 @@ size_t head_ws_layout(int64_t n, int64_t v, void* base, HeadWs* out) {
 
 struct BwdPlan {
   int mt, ct, ksplit, kt_total, grid;
-  int xa, xb;  // XCD block (dh_kernel's tile order), 0 = unblocked
+  int ct_main;  // column tiles of W_lm; the rest (r > 0) are w2's
+  int xa, xb;   // XCD block (dh_kernel's tile order), 0 = unblocked
 };
 
-BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d) {
+BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   BwdPlan pl;
   pl.mt = (int)((n + BM - 1) / BM);
-  pl.ct = (int)((d + BN - 1) / BN);
+  pl.ct_main = (int)((d + BN - 1) / BN);
+  pl.ct = pl.ct_main + (int)((r + BN - 1) / BN);
   pl.kt_total = (int)((v + BK - 1) / BK);
   const int tiles = pl.mt * pl.ct;
   const int cus = device_cus();
@@ -1088,22 +1059,32 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
   return head_forward_typed<float>(p, pl, a, row_stats, metrics, w, st);
 }
 
-size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d) {
-  const BwdPlan pl = bwd_plan(n, v, d);
-  return align_up((size_t)pl.ksplit * n * d * sizeof(float), 256);
+size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r) {
+  const BwdPlan pl = bwd_plan(n, v, d, r);
+  return align_up((size_t)pl.ksplit * n * d * sizeof(float), 256) +
+         align_up((size_t)pl.ksplit * n * r * sizeof(float), 256);
 }
 
 hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
                            int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st) {
+  return lmhead_backward_ext(dl, ldd, weight, ldw, nullptr, 0, 0, dh, lddh, nullptr, n, v, d, ws, st);
+}
+
+hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const void* w2,
+                               int64_t ldw2, int64_t r, void* dh, int64_t lddh, float* dprev, int64_t n, int64_t v,
+                               int64_t d, void* ws, hipStream_t st) {
   if (n == 0 || d == 0) return hipSuccess;
-  const BwdPlan pl = bwd_plan(n, v, d);
+  const BwdPlan pl = bwd_plan(n, v, d, r);
   BwdParams p = {};
   p.dl = static_cast<const uint16_t*>(dl);
   p.weight = static_cast<const uint16_t*>(weight);
   p.ldd = ldd; p.ldw = ldw; p.n = n; p.v = v; p.d = d;
   p.mt = pl.mt; p.ct = pl.ct; p.ksplit = pl.ksplit; p.kt_total = pl.kt_total;
+  p.ct_main = pl.ct_main;
   p.xa = pl.xa; p.xb = pl.xb;
   p.part = static_cast<float*>(ws);
+  p.w2 = static_cast<const uint16_t*>(w2); p.ldw2 = ldw2; p.r = r;
+  p.part2 = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)pl.ksplit * n * d * sizeof(float), 256));
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dh_kernel),
@@ -1117,11 +1098,22 @@ hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int6
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const int64_t quads = (n * d + 3) / 4;
-  NS_TIMED("dh_reduce", st);
-  hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p.part, pl.ksplit,
-                     n, d, static_cast<uint16_t*>(dh), lddh);
-  return hipGetLastError();
+  {
+    const int64_t quads = (n * d + 3) / 4;
+    NS_TIMED("dh_reduce", st);
+    hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p.part, pl.ksplit,
+                       n, d, static_cast<uint16_t*>(dh), lddh);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (r > 0) {
+    const int64_t quads = (n * r + 3) / 4;
+    NS_TIMED("dprev_reduce", st);
+    hipLaunchKernelGGL(sum_partials_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p.part2,
+                       pl.ksplit, n, r, dprev, r);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
 hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,

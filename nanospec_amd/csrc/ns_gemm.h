@@ -14,6 +14,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kNumXcd = 8;   // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
@@ -66,6 +67,62 @@ struct DmaTile {
                                      16, 0, 0);
   }
 };
+
+// B operand [K rows, cols] (cols contiguous) fetched straight into a row-major LDS
+// stage: 64 K rows of 512 bytes, the 16-byte chunk cn of row k stored at physical
+// chunk cn ^ (4 (k & 3)), which keeps the transposed fragment reads (tr_b16) free of
+// bank conflicts.  Instruction i of wave wv fills rows 2 (wv * 8 + i) + {0, 1}; lane l
+// writes physical chunk l % 32 of row 2 (wv * 8 + i) + l / 32.  Column chunks at or
+// past cmax re-read the tile's first chunk (discarded by the caller).
+struct DmaTileKN {
+  uint32_t off[8];
+  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 2 * (wv * 8 + i) + (lane >> 5);
+      const int cn = (lane & 31) ^ (4 * (row & 3));
+      int64_t col = c0 + cn * 8;
+      col = col < cmax ? col : c0;
+      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
+                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * 8 + i) * 1024),
+                                     16, 0, 0);
+  }
+};
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// B fragment i (32 columns) of step kk from a DmaTileKN stage, as two transposed reads:
+// ds_read_b64_tr_b16 gives lane 16 g + x of a 16-lane group element x % 4 of the
+// 8-byte pieces addressed by lanes 16 g + 4 j + x / 4, j = 0..3.  Lane 16 g + 4 j + m
+// addresses row kbase + j, columns nb + 4 m .. +3, so lane 16 g + x receives
+// B[kbase + 0..3][nb + x]: K-contiguous, as the MFMA B operand wants.
+struct TrFrag {
+  i16x4_t lo, hi;  // K 0..3 and 4..7 of this lane's eight
+};
+
+__device__ __forceinline__ uint32_t tr_base(int wn, int i) {
+  // byte address of this lane's piece for step 0, half 0 (add 2048 for half 1, 8192 per step)
+  const int lane = threadIdx.x & 63;
+  const int x = lane & 15;
+  const int row = 8 * (lane >> 5) + (x >> 2);                       // + 16 kk + 4 half
+  const int col = wn * 128 + i * 32 + 16 * ((lane >> 4) & 1) + 4 * (x & 3);
+  const int cn = (col >> 3) ^ (4 * (row & 3));
+  return (uint32_t)(row * 512 + (cn << 4) + (col & 7) * 2);
+}
+
+__device__ __forceinline__ i16x4_t tr_read(const lds_t* buf, uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) i16x4_t*>(const_cast<lds_t*>(buf) + addr));
+}
+
+__device__ __forceinline__ bf16x8_t tr_join(const TrFrag& f) {
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(f.lo, f.hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 // Wait for this wave's LDS fills and all outstanding memory operations, then a
 // workgroup barrier.  The empty asm statements keep the compiler from moving memory

@@ -51,9 +51,20 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
                           const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
                           int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd,
                           float* row_stats, float* metrics, void* ws, hipStream_t st);
-size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d);
+// dh workspace; r > 0 adds the Markov column tiles' partials
+size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r = 0);
 hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh,
                            int64_t lddh, int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st);
+// dh = dl . weight and, when r > 0, dprev = dl . w2 (fp32 [N, r], row stride r) in the same GEMM
+hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const void* w2,
+                               int64_t ldw2, int64_t r, void* dh, int64_t lddh, float* dprev, int64_t n, int64_t v,
+                               int64_t d, void* ws, hipStream_t st);
+// Markov-head backward (markov.hip): dh, w2_grad = dl^T . w1[prev] (overwritten) and
+// w1_grad.index_add_(prev, dl . w2) (accumulated, deterministic order)
+size_t markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r);
+hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const MarkovFactors& f,
+                           void* dh, int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2,
+                           int64_t n, int64_t v, int64_t d, void* ws, size_t ws_bytes, hipStream_t st);
 hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                          int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d,
                          hipStream_t st);

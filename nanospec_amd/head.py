@@ -144,10 +144,51 @@ def lm_head_linear_backward(dl, lm_head_weight):
     return dh.view(tuple(dl.shape[:-1]) + (d,))
 
 
+def _grad_rows(t: torch.Tensor, vocab: int, r: int, name: str):
+    """A [V, r] bf16 gradient buffer written in place: rows must be unit-stride."""
+    if t.dtype != torch.bfloat16 or t.dim() != 2 or tuple(t.shape) != (vocab, r):
+        raise ValueError(f"{name} must be bfloat16 [{vocab}, {r}] (got {t.dtype} {tuple(t.shape)})")
+    if t.stride(1) != 1 or t.stride(0) < r:
+        raise ValueError(f"{name} must have unit-stride rows to be written in place")
+    return t, t.stride(0)
+
+
 @torch.no_grad()
-def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, return_dlogits=False):
+def lm_head_markov_backward(dl, lm_head_weight, markov: MarkovFactors, w1_grad, w2_grad):
+    """The head backward with the factored Markov head (train.py:302-307):
+    dh = dl . W_lm; markov_w2.grad = dl^T . w1[previous] (overwritten, as
+    ops.linear_backward's copy_, ops.py:38-45); markov_w1.grad.index_add_(previous,
+    dl . w2) (accumulated, ops.embedding_backward, ops.py:73-74).  d(previous) stays
+    fp32 inside the library and each w1.grad row gets its tokens' sum in token order.
+    Returns dh [..., d] bf16."""
+    vocab, d = lm_head_weight.shape
+    device = _lib.require_device(dl, lm_head_weight, markov.w1, markov.w2, w1_grad, w2_grad)
+    g, ldg = _bf16_rows(dl, vocab, "dl")
+    w, ldw = _bf16_rows(lm_head_weight, d, "lm_head_weight")
+    n = g.shape[0]
+    prev, w1, ldw1, w2, ldw2, r = _markov_inputs(markov, vocab, n, device)
+    g1, ldg1 = _grad_rows(w1_grad, vocab, r, "w1_grad")
+    g2, ldg2 = _grad_rows(w2_grad, vocab, r, "w2_grad")
+    lib = _lib.load()
+    dh = torch.empty((n, d), dtype=torch.bfloat16, device=device)
+    nbytes = int(lib.ns_lmhead_markov_bwd_workspace_bytes(n, vocab, d, r))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    status = lib.ns_lmhead_markov_bwd(
+        _lib.ptr(g), ldg, _lib.ptr(w), ldw, _lib.ptr(prev), _lib.ptr(w1), ldw1, _lib.ptr(w2), ldw2, r,
+        _lib.ptr(dh), d, _lib.ptr(g1), ldg1, _lib.ptr(g2), ldg2, n, vocab, d, _lib.ptr(ws), ws.numel(),
+        _lib.stream(device),
+    )
+    _lib.check(status, "ns_lmhead_markov_bwd")
+    return dh.view(tuple(dl.shape[:-1]) + (d,))
+
+
+@torch.no_grad()
+def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, return_dlogits=False,
+                           markov_grads=None):
     """dh = dl . W_lm with the dl emitted by the forward.  Returns dh [..., d] bf16
-    (and dl [..., V] bf16 when ``return_dlogits``, for the Markov backward)."""
+    (and dl [..., V] bf16 when ``return_dlogits``, for the Markov backward).
+    ``markov_grads=(w1_grad, w2_grad)`` with a factored Markov forward also runs the
+    Markov-head backward in the same GEMM (``lm_head_markov_backward``)."""
     if saved.dlogits is None:
         raise ValueError("no dl to propagate: the forward ran with emit_dlogits=False, or the backward already ran")
     if accumulation_steps != saved.accumulation_steps:
@@ -156,7 +197,12 @@ def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, retu
             "to lm_head_ce_kl_loss and lm_head_ce_kl_backward"
         )
     dl, saved.dlogits = saved.dlogits, None   # handed over once, so it is freed after dh unless returned
-    dh = lm_head_linear_backward(dl, saved.weight)
+    if markov_grads is not None:
+        if saved.markov is None:
+            raise ValueError("markov_grads given, but the forward ran without Markov factors")
+        dh = lm_head_markov_backward(dl, saved.weight, saved.markov, *markov_grads)
+    else:
+        dh = lm_head_linear_backward(dl, saved.weight)
     dl = dl.view(saved.shape)
     dh = dh.view(saved.shape[:-1] + (saved.weight.shape[1],))
     return (dh, dl) if return_dlogits else dh
@@ -186,10 +232,13 @@ def lm_head_linear(x, lm_head_weight, addend=None):
 
 @torch.no_grad()
 def head_step(hidden, lm_head_weight, target_logits, prepared, objective, *, markov_logits=None,
-              accumulation_steps=1):
+              markov=None, markov_grads=None, accumulation_steps=1):
     """The head region of train() (train.py:268-312) on the fused path: returns
-    (LossMetrics, dh, dl); dl feeds the Markov-head backward (train.py:303-307)."""
+    (LossMetrics, dh, dl); dl feeds the Markov-head backward (train.py:303-307).
+    With ``markov`` factors and ``markov_grads=(w1_grad, w2_grad)`` that backward runs
+    here too, and the gradient buffers are updated in place."""
     metrics, saved = lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objective,
-                                        markov_logits=markov_logits, accumulation_steps=accumulation_steps)
-    dh, dl = lm_head_ce_kl_backward(saved, accumulation_steps, return_dlogits=True)
+                                        markov_logits=markov_logits, markov=markov,
+                                        accumulation_steps=accumulation_steps)
+    dh, dl = lm_head_ce_kl_backward(saved, accumulation_steps, return_dlogits=True, markov_grads=markov_grads)
     return metrics, dh, dl

@@ -87,3 +87,107 @@ def test_markov_bad_previous_id_poisons_its_row(gpu_lib):
     ce = _np(saved.row_stats)[:, 2]
     assert np.isnan(ce[5]) and np.all(np.isfinite(np.delete(ce, 5)))
     assert np.isnan(float(m.ce))
+
+
+# ---------------------------------------------------------------------------
+# backward: dh, markov_w2.grad (copy_) and markov_w1.grad (index_add_), train.py:302-307
+# ---------------------------------------------------------------------------
+
+
+def _bwd_inputs(n, v, d, r, seed, id_range=None):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    dl = (1e-3 * torch.randn((n, v), generator=g, device=DEV)).bfloat16()
+    w = (0.02 * torch.randn((v, d), generator=g, device=DEV)).bfloat16()
+    prev, w1, w2 = synthetic.markov_factors(n, v, r, seed + 1, DEV)
+    if id_range is not None:
+        prev = torch.randint(0, id_range, (n,), generator=g, device=DEV)
+    g1 = (1e-3 * torch.randn((v, r), generator=g, device=DEV)).bfloat16()   # accumulated into
+    return dl, w, head.MarkovFactors(prev, w1, w2), g1
+
+
+def _run_bwd(dl, w, mk, g1):
+    w1_grad = g1.clone()
+    w2_grad = torch.full_like(g1, float("nan"))          # overwritten, never read
+    dh = head.lm_head_markov_backward(dl, w, mk, w1_grad, w2_grad)
+    torch.cuda.synchronize()
+    return dh, w1_grad, w2_grad
+
+
+def _assert_grads(dl, mk, g1, w1_grad, w2_grad, keep=None):
+    """w2.grad and w1.grad against the fp64 oracle.  Each is one bf16 rounding of an
+    fp32 sum: within 2^-8 relative plus fp32 accumulation error, bounded by 2^-18 of
+    the same sum taken over absolute values."""
+    dln, prev = _np(dl).astype(np.float64), mk.previous.cpu().numpy()
+    w1n, w2n = _np(mk.w1).astype(np.float64), _np(mk.w2).astype(np.float64)
+    if keep is None:
+        keep = np.ones(len(prev), dtype=bool)
+    dprev, dw2, dw1 = ref.markov_backward(dln[keep], prev[keep], w1n, w2n)
+    scale2 = np.abs(dln[keep]).T @ np.abs(w1n[prev[keep]])
+    got2 = _np(w2_grad)
+    assert np.all(np.abs(got2 - dw2) <= np.abs(dw2) * 2.0 ** -8 + 2.0 ** -18 * scale2 + 1e-30), \
+        float(np.abs(got2 - dw2).max())
+    want1 = _np(g1).astype(np.float64) + dw1
+    scale1 = np.zeros_like(dw1)
+    np.add.at(scale1, prev[keep], np.abs(dln[keep]) @ np.abs(w2n))
+    got1 = _np(w1_grad)
+    assert np.all(np.abs(got1 - want1) <= np.abs(want1) * 2.0 ** -8 + 2.0 ** -18 * scale1 + 1e-30), \
+        float(np.abs(got1 - want1).max())
+
+
+@pytest.mark.parametrize("n,v,d,r,id_range", [
+    (72, 8200, 128, 64, None),        # ragged vocab tile, a 64-token stage plus an 8-token tail
+    (256, 4096, 256, 256, None),      # the reference rank, whole stages only
+    (1000, 2048, 192, 128, 16),       # long runs of repeated ids (index_add_ segments of ~60)
+    (1536, 16384, 256, 256, None),    # 24 token stages, 64 vocab tiles
+])
+def test_markov_backward_matches_oracle(gpu_lib, n, v, d, r, id_range):
+    dl, w, mk, g1 = _bwd_inputs(n, v, d, r, 60 + n, id_range)
+    dh, w1_grad, w2_grad = _run_bwd(dl, w, mk, g1)
+    dh_ref = ref.lm_head_backward(_np(dl), _np(w), dtype=np.float32 if n > 1024 else np.float64)
+    sim = ref.similarity(_np(dh), dh_ref)
+    assert sim["cosine_min"] >= 0.9999 and sim["max_abs"] <= 2e-2 * np.abs(dh_ref).max(), sim
+    _assert_grads(dl, mk, g1, w1_grad, w2_grad)
+
+
+def test_markov_backward_deterministic(gpu_lib):
+    dl, w, mk, g1 = _bwd_inputs(2048, 8192, 256, 256, 5, id_range=64)
+    a = _run_bwd(dl, w, mk, g1)
+    b = _run_bwd(dl, w, mk, g1)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_markov_backward_skips_out_of_range_ids(gpu_lib):
+    """Rows with a prev id outside [0, V) add nothing to w1.grad (the forward has made
+    their loss NaN); dh does not depend on prev."""
+    n, v, d, r = 128, 2048, 128, 64
+    dl, w, mk, g1 = _bwd_inputs(n, v, d, r, 11)
+    mk.previous[3] = v
+    mk.previous[77] = -1
+    dh, w1_grad, w2_grad = _run_bwd(dl, w, mk, g1)
+    keep = np.ones(n, dtype=bool)
+    keep[[3, 77]] = False
+    dln, prev = _np(dl).astype(np.float64), mk.previous.cpu().numpy()
+    _, _, dw1 = ref.markov_backward(dln[keep], prev[keep], _np(mk.w1), _np(mk.w2))
+    want1 = _np(g1).astype(np.float64) + dw1
+    assert np.all(np.abs(_np(w1_grad) - want1) <= np.abs(want1) * 2.0 ** -8 + 1e-6)
+    sim = ref.similarity(_np(dh), ref.lm_head_backward(_np(dl), _np(w)))
+    assert sim["cosine_min"] >= 0.9999, sim
+
+
+def test_markov_forward_backward_through_head_step(gpu_lib):
+    """head_step with factors: the backward's gradients follow the dl the forward emitted."""
+    n, d, v, r = 256, 256, 4096, 256
+    hidden, weight, teacher, slots, mk = _inputs(n, d, v, r, 21)
+    o = Objective(block_size=8)
+    g1 = torch.zeros((v, r), dtype=torch.bfloat16, device=DEV)
+    w1_grad, w2_grad = g1.clone(), torch.empty_like(g1)
+    m, dh, dl = head.head_step(hidden, weight, teacher, slots, o, markov=mk, markov_grads=(w1_grad, w2_grad))
+    torch.cuda.synchronize()
+    dl2 = dl.reshape(n, v)
+    _, _, _, dl_ref = _oracle(hidden, weight, teacher, slots, mk, o)
+    diff = np.abs(_np(dl2).astype(np.float64) - dl_ref)
+    assert np.all(diff <= np.abs(dl_ref) * 2.0 ** -7 + 2e-5 * np.abs(dl_ref).max(axis=-1, keepdims=True))
+    _assert_grads(dl2, mk, g1, w1_grad, w2_grad)
+    sim = ref.similarity(_np(dh).reshape(n, d), ref.lm_head_backward(_np(dl2), _np(weight)))
+    assert sim["cosine_min"] >= 0.9999, sim
