@@ -808,12 +808,14 @@ struct BwdParams {
   int mt, ct, ksplit;      // token tiles, d tiles, K splits
   int xa, xb;              // XCD block: xa token tiles x xb d tiles per round (0 = unblocked)
   int kt_total;            // ceil(V / BK)
+  int grid_main;           // mt * ct * ksplit workgroups of dh tiles
   float* part;             // [ksplit][N][d] fp32
-  // Markov extension (r > 0): column tiles ct >= ct_main multiply by w2 [V, r]
-  // instead, into part2 [ksplit][N][r] (d(previous) = dl . w2)
+  // Markov extension (r > 0): workgroups past grid_main take mt x ct2 column tiles of
+  // w2 [V, r] with their own K split count ksplit2, into part2 [ksplit2][N][r]
+  // (d(previous) = dl . w2)
   const uint16_t* w2;
   int64_t ldw2, r;
-  int ct_main;
+  int ct2, ksplit2;
   float* part2;
 };
 
@@ -826,10 +828,17 @@ void dh_kernel(BwdParams p) {
   // xa token tiles x xb d tiles of one K split, so a K stage reads xa + xb distinct
   // operand tiles through that XCD's L2; blocks are numbered token group fastest, then
   // d group, then K split.  xa = 0: consecutive ids per XCD, token tile fastest.
-  const int G = gridDim.x;
+  const int G = p.grid_main;
   const int g = blockIdx.x;
-  int mt, ct, ks;
-  if (p.xa > 0) {
+  int mt, ct, ks, nsplit = p.ksplit;
+  const bool mk = g >= G;   // a Markov column tile (after every dh tile)
+  if (mk) {
+    const int q = g - G;
+    mt = q % p.mt;
+    ct = (q / p.mt) % p.ct2;
+    ks = q / (p.mt * p.ct2);
+    nsplit = p.ksplit2;
+  } else if (p.xa > 0) {
     const int C = p.xa * p.xb;
     const int i = g / kNumXcd;
     const int blk = (i / C) * kNumXcd + g % kNumXcd, r = i % C;
@@ -845,14 +854,13 @@ void dh_kernel(BwdParams p) {
     ct = rest % p.ct;
     ks = rest / p.ct;
   }
-  const int kt0 = (int)((int64_t)ks * p.kt_total / p.ksplit);
-  const int kt1 = (int)((int64_t)(ks + 1) * p.kt_total / p.ksplit);
+  const int kt0 = (int)((int64_t)ks * p.kt_total / nsplit);
+  const int kt1 = (int)((int64_t)(ks + 1) * p.kt_total / nsplit);
   // the column tile reads W_lm, or w2 for the Markov extension tiles
-  const bool mk = ct >= p.ct_main;
   const uint16_t* B = mk ? p.w2 : p.weight;
   const int64_t ldb = mk ? p.ldw2 : p.ldw;
   const int64_t cols = mk ? p.r : p.d;
-  const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)(mk ? ct - p.ct_main : ct) * BN;
+  const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)ct * BN;
   f32x16_t acc[4][4];
   zero_acc(acc);
   // full stages straight into LDS; a partial last stage (V % BK != 0) through registers,
@@ -964,16 +972,16 @@ size_t head_ws_layout(int64_t n, int64_t v, void* base, HeadWs* out) {
 }
 
 struct BwdPlan {
-  int mt, ct, ksplit, kt_total, grid;
-  int ct_main;  // column tiles of W_lm; the rest (r > 0) are w2's
-  int xa, xb;   // XCD block (dh_kernel's tile order), 0 = unblocked
+  int mt, ct, ksplit, kt_total, grid_main, grid;
+  int ct2, ksplit2;  // Markov column tiles (r > 0) and their K splits
+  int xa, xb;        // XCD block (dh_kernel's tile order), 0 = unblocked
 };
 
 BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   BwdPlan pl;
   pl.mt = (int)((n + BM - 1) / BM);
-  pl.ct_main = (int)((d + BN - 1) / BN);
-  pl.ct = pl.ct_main + (int)((r + BN - 1) / BN);
+  pl.ct = (int)((d + BN - 1) / BN);
+  pl.ct2 = (int)((r + BN - 1) / BN);
   pl.kt_total = (int)((v + BK - 1) / BK);
   const int tiles = pl.mt * pl.ct;
   const int cus = device_cus();
@@ -982,7 +990,20 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   if (ks > 16) ks = 16;
   if (ks > pl.kt_total) ks = pl.kt_total;
   pl.ksplit = ks;
-  pl.grid = tiles * ks;
+  pl.grid_main = tiles * ks;
+  // Markov tiles run after the dh tiles as one extra round: enough K splits to give
+  // every CU one (each then covers a fraction of V), at least the dh count
+  pl.ksplit2 = 0;
+  pl.grid = pl.grid_main;
+  if (pl.ct2 > 0) {
+    const int tiles2 = pl.mt * pl.ct2;
+    int ks2 = (cus + tiles2 - 1) / tiles2;
+    if (ks2 < ks) ks2 = ks;
+    if (ks2 > 64) ks2 = 64;
+    if (ks2 > pl.kt_total) ks2 = pl.kt_total;
+    pl.ksplit2 = ks2;
+    pl.grid += tiles2 * ks2;
+  }
   // XCD block (dh_kernel's tile order): xa * xb = CUs per XCD, xa | mt, xb | ct, whole
   // rounds on every XCD; the smallest xa + xb
   pl.xa = pl.xb = 0;
@@ -990,7 +1011,7 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
     const int C = cus / kNumXcd;
     for (int a = 1; a <= C; ++a) {
       const int b = C / a;
-      if (C % a || pl.mt % a || pl.ct % b || pl.grid % (kNumXcd * C)) continue;
+      if (C % a || pl.mt % a || pl.ct % b || pl.grid_main % (kNumXcd * C)) continue;
       if (pl.xa == 0 || a + b < pl.xa + pl.xb) { pl.xa = a; pl.xb = b; }
     }
   }
@@ -1062,7 +1083,7 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
 size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r) {
   const BwdPlan pl = bwd_plan(n, v, d, r);
   return align_up((size_t)pl.ksplit * n * d * sizeof(float), 256) +
-         align_up((size_t)pl.ksplit * n * r * sizeof(float), 256);
+         align_up((size_t)pl.ksplit2 * n * r * sizeof(float), 256);
 }
 
 hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
@@ -1080,7 +1101,7 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
   p.weight = static_cast<const uint16_t*>(weight);
   p.ldd = ldd; p.ldw = ldw; p.n = n; p.v = v; p.d = d;
   p.mt = pl.mt; p.ct = pl.ct; p.ksplit = pl.ksplit; p.kt_total = pl.kt_total;
-  p.ct_main = pl.ct_main;
+  p.grid_main = pl.grid_main; p.ct2 = pl.ct2; p.ksplit2 = pl.ksplit2;
   p.xa = pl.xa; p.xb = pl.xb;
   p.part = static_cast<float*>(ws);
   p.w2 = static_cast<const uint16_t*>(w2); p.ldw2 = ldw2; p.r = r;
@@ -1110,7 +1131,7 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
     const int64_t quads = (n * r + 3) / 4;
     NS_TIMED("dprev_reduce", st);
     hipLaunchKernelGGL(sum_partials_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p.part2,
-                       pl.ksplit, n, r, dprev, r);
+                       pl.ksplit2, n, r, dprev, r);
     return hipGetLastError();
   }
   return hipSuccess;
