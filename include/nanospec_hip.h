@@ -11,6 +11,8 @@
  *   nanospec/train.py:276-279 (MarkovHead, layers.py:74-78: embedding + linear)
  *     fused into the LM head as a second K segment -> ns_lmhead_markov_ce_kl_fwd
  *   nanospec/train.py:302-307     dh, markov_w2.grad, markov_w1.grad -> ns_lmhead_markov_bwd
+ *   nanospec/train.py:525-535, shard.py:318-330  pooled metrics, gradient factor
+ *                                 -> ns_pooled_tail, ns_scale_gradient
  *
  * Conventions
  *   - All tensor arguments are device pointers; rows are `ld` elements apart,
@@ -130,6 +132,18 @@ int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_
                          const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r, void* dh,
                          int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2, int64_t n, int64_t v,
                          int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+
+/* Pooled-normalisation tail (train.py:525-535, shard.py:318-327): sums `count` LossMetrics
+ * buffers metrics [count][6] in index order (the reference all-reduces numerator,
+ * denominator, accept_len_sum and accept_len_total over ranks) and writes out fp32 [4] =
+ * (loss = num / max(den, 1e-6), accept_len = sum / max(total, 1),
+ *  gradient factor = den > 0 ? world_size * accumulation_steps / max(den, 1e-6) : 0, den). */
+int ns_pooled_tail(const float* metrics, int64_t count, int64_t world_size, int64_t accumulation_steps, float* out,
+                   ns_stream_t stream);
+
+/* grad[0..n) *= *factor in place, the factor read on the device (shard.py:330,
+ * shard.grad.mul_(factor)); grad bf16 (rounded once) or fp32, 16-byte aligned. */
+int ns_scale_gradient(void* grad, int dtype, int64_t n, const float* factor, ns_stream_t stream);
 
 /* Plain LM-head projection out = x . weight^T (+ addend), bf16 out (ops.py:34-35 for
  * the head: train.py:272, 279, 284).  x [N, d], weight [V, d], addend [N, V] or NULL. */

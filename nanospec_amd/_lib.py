@@ -53,13 +53,15 @@ SIGNATURES = {
         _I,
     ),
     "ns_lmhead_bwd": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
-    "ns_lmhead_linear": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], _I),
     "ns_lmhead_markov_bwd_workspace_bytes": ([_I64, _I64, _I64, _I64], _SZ),
     "ns_lmhead_markov_bwd": (
         [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
          _P, _SZ, _P],
         _I,
     ),
+    "ns_pooled_tail": ([_P, _I64, _I64, _I64, _P, _P], _I),
+    "ns_scale_gradient": ([_P, _I, _I64, _P, _P], _I),
+    "ns_lmhead_linear": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], _I),
     "ns_fp8_teacher_logits": ([_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "ns_fp8_quantize_rows": ([_P, _I64, _I64, _I64, _P, _P, _P], _I),
     "ns_prepare_slots": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _P], _I),

@@ -247,6 +247,26 @@ int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_
                     "ns_lmhead_markov_bwd");
 }
 
+int ns_pooled_tail(const float* metrics, int64_t count, int64_t world_size, int64_t accumulation_steps, float* out,
+                   ns_stream_t stream) {
+  if (count < 1) return fail(NS_EINVAL, "count must be >= 1 (got %lld)", (long long)count);
+  if (world_size < 1 || accumulation_steps < 1 || world_size * accumulation_steps > (int64_t(1) << 24))
+    return fail(NS_EINVAL, "world_size and accumulation_steps must be >= 1 with a product <= 2^24");
+  if (!metrics || !out) return fail(NS_ENULL, "metrics and out must be non-NULL");
+  return hip_status(ns::pooled_tail(metrics, count, world_size, accumulation_steps, out,
+                                    reinterpret_cast<hipStream_t>(stream)),
+                    "ns_pooled_tail");
+}
+
+int ns_scale_gradient(void* grad, int dtype, int64_t n, const float* factor, ns_stream_t stream) {
+  if (!dtype_ok(dtype)) return fail(NS_EDTYPE, "unsupported gradient dtype code %d", dtype);
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (n > 0 && (!grad || !factor)) return fail(NS_ENULL, "grad and factor must be non-NULL");
+  if (!aligned(grad)) return fail(NS_EALIGN, "grad must be 16-byte aligned");
+  return hip_status(ns::scale_gradient(grad, dtype, n, factor, reinterpret_cast<hipStream_t>(stream)),
+                    "ns_scale_gradient");
+}
+
 int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                      int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, ns_stream_t stream) {
   if (n < 0) return fail(NS_EINVAL, "n must be >= 0");

@@ -83,6 +83,13 @@ hipError_t prepare_slots(const int64_t* ids, const float* loss_mask, const int64
                          float gamma, int64_t* target_ids, int64_t* previous, float* weights,
                          uint8_t* valid, int64_t* teacher_indices, hipStream_t st);
 
+// ---- pooled-normalisation tail (pooled.hip) ------------------------------------
+// out[4] = (loss, accept_len, gradient factor, pooled denominator) from [count][6] metrics
+hipError_t pooled_tail(const float* metrics, int64_t count, int64_t world_size, int64_t accumulation_steps,
+                       float* out, hipStream_t st);
+// grad[0..n) *= *factor in place (bf16 or fp32)
+hipError_t scale_gradient(void* grad, int dtype, int64_t n, const float* factor, hipStream_t st);
+
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 }  // namespace ns

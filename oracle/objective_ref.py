@@ -26,6 +26,13 @@ markov_logits / backward   torch F.embedding + F.linear forward, torch.autograd
                            for d(previous), d(w2) and the index_add d(w1);
                            hand-worked index_add with repeated ids
 slot_preparation           hand-computed known answers; brute-force loops
+pooled_tail                hand-computed known answers (den = 0 -> factor 0 and
+                           the 1e-6 clamp; accept total 0 -> clamp 1); torch's
+                           own evaluation of shard.py:321-327 on fp32 tensors;
+                           factor * den == world * acc
+scale_gradient             torch products (bit-exact, CPU): fp32 x fp32 factor;
+                           bf16 x bf16-cast factor; the device semantics of
+                           bf16.mul_(0-d fp32) against torch's device mul_ (GPU)
 e4m3 round / fp8_linear    torch ``float8_e4m3fn`` cast; exact products for
                            e4m3-grid inputs with power-of-two scales
 bf16_round                 torch ``bfloat16`` cast
@@ -319,6 +326,43 @@ def markov_backward(dl, prev, w1, w2, dtype=np.float64):
     dw1 = np.zeros(np.shape(w1), dtype=dtype)
     np.add.at(dw1, prev, dprev)
     return dprev, dw2, dw1
+
+
+# ---------------------------------------------------------------------------
+# Pooled-normalisation tail  train.py:525-535, shard.py:318-330
+# ---------------------------------------------------------------------------
+
+
+def pooled_tail(metrics, world_size=1, accumulation_steps=1):
+    """Pool [count, 6] LossMetrics buffers (ce, kl, numerator, denominator, accept_len_sum,
+    accept_len_total) in fp32 in index order, as the training loop's all-reduce of the last
+    four (train.py:525-532) does across ranks; then loss = num / max(den, 1e-6) and
+    accept_len = sum / max(total, 1) (train.py:533-534), and the gradient factor of
+    adamw_step (shard.py:321-327): world * acc / max(den, 1e-6) if den > 0 else 0, where
+    the int-over-tensor division is reciprocal(max(den, 1e-6)) * (world * acc) in fp32.
+    Returns fp32 (loss, accept_len, factor, den)."""
+    m = np.asarray(metrics, dtype=np.float32).reshape(-1, 6)
+    num = den = asum = atot = np.float32(0.0)
+    for row in m:
+        num = np.float32(num + row[2])
+        den = np.float32(den + row[3])
+        asum = np.float32(asum + row[4])
+        atot = np.float32(atot + row[5])
+    loss = np.float32(num / max(den, np.float32(1e-6)))
+    accept = np.float32(asum / max(atot, np.float32(1.0)))
+    wa = np.float32(world_size * accumulation_steps)
+    factor = np.float32(np.float32(1.0) / max(den, np.float32(1e-6)) * wa) if den > 0 else np.float32(0.0)
+    return loss, accept, factor, den
+
+
+def scale_gradient(grad, factor, bf16=False):
+    """grad.mul_(factor) (shard.py:330) with a 0-d fp32 factor: for bf16 gradients
+    (shard.py:74, zeros_like of the bf16 parameter) torch casts the factor to bf16 first,
+    multiplies in fp32 and rounds the product to bf16; fp32 gradients multiply directly."""
+    g = np.asarray(grad, dtype=np.float32)
+    if bf16:
+        return bf16_round(g * bf16_round(np.float32(factor)))
+    return g * np.float32(factor)
 
 
 # ---------------------------------------------------------------------------

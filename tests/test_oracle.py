@@ -336,3 +336,62 @@ def test_similarity_metrics():
     z = np.array([[0.0, 0.0], [1.0, 1.0]])
     assert ref.similarity(z, z)["cosine_min"] == pytest.approx(1.0)
     assert ref.similarity(np.array([[1e-3, 0.0], [1.0, 1.0]]), z)["zero_rows_nonzero"] == 1
+
+
+# --------------------------------------------------------------- pooled tail
+
+
+def test_pooled_tail_hand_worked():
+    """Two buffers: num 3 + 1, den 2 + 2, accept 10 + 6 over 4 + 4 blocks; world 2, acc 3."""
+    m = np.array([[0.5, 0.25, 3.0, 2.0, 10.0, 4.0], [0.7, 0.1, 1.0, 2.0, 6.0, 4.0]], np.float32)
+    loss, accept, factor, den = ref.pooled_tail(m, world_size=2, accumulation_steps=3)
+    assert (loss, accept, factor, den) == (1.0, 2.0, 1.5, 4.0)
+    # nothing supervised: factor 0, the 1e-6 clamp on the loss, accept total clamped to 1
+    loss, accept, factor, den = ref.pooled_tail([[0, 0, 0.5, 0, 0, 0]], 4, 2)
+    assert factor == 0.0 and den == 0.0 and accept == 0.0
+    assert loss == np.float32(np.float32(0.5) / np.float32(1e-6))
+
+
+def test_pooled_tail_matches_torch_evaluation_of_adamw_step():
+    """shard.py:321-327 and train.py:533-534 evaluated by torch on fp32 tensors: the int
+    over tensor division rounds twice (reciprocal, then product), which the oracle keeps."""
+    g = np.random.default_rng(5)
+    mismatch_if_divided = 0
+    for trial in range(400):
+        count = int(g.integers(1, 5))
+        m = np.zeros((count, 6), np.float32)
+        m[:, 2] = g.uniform(0, 50, count)
+        m[:, 3] = g.uniform(0, 7, count) if trial % 10 else 0.0
+        m[:, 4] = g.integers(0, 600, count)
+        m[:, 5] = g.integers(0, 100, count)
+        world, acc = int(g.integers(1, 9)), int(g.integers(1, 9))
+        loss, accept, factor, den = ref.pooled_tail(m, world, acc)
+        pooled = torch.zeros(4, dtype=torch.float32)
+        for row in torch.from_numpy(m):
+            pooled += row[2:]
+        t_den = pooled[1].clone()
+        t_factor = torch.where(t_den > 0, world * acc / t_den.clamp_min(1e-6), 0.0)
+        assert float(pooled[0] / pooled[1].clamp_min(1e-6)) == loss
+        assert float(pooled[2] / pooled[3].clamp_min(1.0)) == accept
+        assert float(t_factor) == factor and float(t_den) == den
+        if den > 0 and np.float32(world * acc) / max(den, np.float32(1e-6)) != factor:
+            mismatch_if_divided += 1
+        if den >= 1e-6:
+            assert abs(float(factor) * float(den) - world * acc) <= 1e-6 * world * acc
+    # the two-rounding form is observable: a plain division would differ on some inputs
+    assert mismatch_if_divided > 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_scale_gradient_matches_torch_mul(dtype):
+    """shard.py:330 grad.mul_(factor), bit-exact against torch's own products: fp32 times
+    the 0-d fp32 factor; bf16 times the factor cast to bf16 (what the device kernel of
+    mul_ computes for a bf16 tensor and a 0-d fp32 device tensor -- torch's CPU kernel
+    keeps the fp32 factor instead, so the device semantics are pinned by the GPU test
+    against torch's device mul_)."""
+    g = torch.randn(5000, generator=torch.Generator().manual_seed(2)).to(dtype)
+    for f in (1.0 / 3.7, 0.0, 2.0 ** -20 * 1.2345, 7.0):
+        factor = torch.tensor(f, dtype=torch.float32)
+        want = g.clone().mul_(factor.to(dtype)).float().numpy()
+        got = ref.scale_gradient(g.float().numpy(), factor.item(), bf16=dtype == torch.bfloat16)
+        assert np.array_equal(got, want), f
