@@ -33,7 +33,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c2m"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c2x"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU-baseline sample (0: default)")
     p.add_argument("--pmc-driver", action="store_true",
@@ -78,13 +78,18 @@ KERNEL_NAMES = [
     (r"dw2_kernel", "markov_dw2"),
     (r"markov_keys_kernel", "markov_sort"),
     (r"markov_scatter_kernel", "markov_scatter"),
+    (r"rms_fwd_kernel", "rms_norm_fwd"),
+    (r"rms_bwd_kernel", "rms_norm_bwd"),
+    (r"rms_wgrad_kernel", "rms_norm_wgrad"),
+    (r"pooled_tail_kernel", "pooled_tail"),
+    (r"scale_kernel", "scale_gradient"),
     (r"fp8_quant_kernel", "fp8_quant"),
     (r"fp8_head_kernel", "fp8_head_gemm"),
     (r"prepare_kernel", "prepare_slots"),
 ]
 # profiles/<prefix>_traffic.md and <prefix>_kernel_stats.md: named for the kernels and workload
 PROFILE_PREFIX = {"c1": "stream_c1", "c2": "lmhead_c2", "c3": "lmhead_c3", "c4": "fp8_lmhead_c4",
-                  "c2m": "markov_lmhead_c2m"}
+                  "c2x": "head_ext_c2x"}
 CALIBRATION_BYTES = 1 << 30   # the --pmc-driver calibration (fp32 negation): reads and writes 1 GiB
 
 
@@ -357,39 +362,50 @@ def workload_head(device, args, which):
                 per_slot_fp8_flops=2.0 * v * d if fp8 is not None else None)
 
 
-# --------------------------------------------------------------------------- C2M
+# --------------------------------------------------------------------------- C2X
 
 
-def workload_c2m(device, args):
-    """C2 with the Markov head in factored form at the reference rank (r = 256,
-    config.py:26) instead of a dense [N, V] addend: the K-extended head GEMM in both
-    passes, then dh and d(previous) in one GEMM, w2.grad and the sorted w1.grad
-    index_add (train.py:276-279, 302-307)."""
+def workload_c2x(device, args):
+    """C2 with the path's neighbours included (train.py:271-310, 525-535; shard.py:
+    318-330): final_norm (ops.rms_norm, weight ones as initialised, dspark.py:64-65) on a
+    pre-norm N(0,1) input before the head and its backward fused after the dh GEMM; the
+    Markov head in factored form at the reference rank (r = 256, config.py:26) instead of
+    a dense [N, V] addend, with its backward (w2.grad copy, w1.grad index_add); the pooled
+    tail and the gradient factor applied to the Markov and norm gradients."""
     import torch
 
-    from nanospec_amd import head, synthetic
+    from nanospec_amd import head, ops, pooled, synthetic
     from nanospec_amd.config import Objective
 
     r = 256
     hidden, weight, markov, teacher, slots = synthetic.c2(device)
     del markov
-    prev, w1, w2 = synthetic.markov_factors(hidden.shape[0], weight.shape[0], r, 2002, device)
+    n, d = hidden.shape
+    v = weight.shape[0]
+    x = torch.randn((n, d), generator=torch.Generator(device=device).manual_seed(3002), device=device).bfloat16()
+    norm_w = torch.ones(d, dtype=torch.bfloat16, device=device)
+    norm_g = torch.zeros_like(norm_w)
+    prev, w1, w2 = synthetic.markov_factors(n, v, r, 2002, device)
     mk = head.MarkovFactors(prev, w1, w2)
     w1_grad = torch.zeros_like(w1)
     w2_grad = torch.zeros_like(w2)
-    n, d = hidden.shape
-    v = weight.shape[0]
     o = Objective(block_size=8, gamma=4.0)
+    del hidden
 
     def step():
-        metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov=mk)
-        dh = head.lm_head_ce_kl_backward(saved, markov_grads=(w1_grad, w2_grad))
-        return metrics, dh
+        w1_grad.zero_()
+        h, saved_norm = ops.rms_norm(x, norm_w, 1e-6)
+        metrics, saved = head.lm_head_ce_kl_loss(h, weight, teacher, slots, o, markov=mk)
+        dx = head.lm_head_ce_kl_backward(saved, markov_grads=(w1_grad, w2_grad),
+                                         final_norm=(saved_norm, norm_w, norm_g))
+        tail = pooled.pooled_tail(metrics)
+        pooled.scale_gradients_((w1_grad, w2_grad, norm_g), tail.factor)
+        return metrics, dx
 
     gemm_k = 2.0 * n * v * (d + r)
     kernel_flops = {"head_stats": gemm_k, "head_emit": gemm_k, "dh_gemm": gemm_k, "markov_dw2": 2.0 * n * v * r}
     kernel_bytes = {"head_stats": 2 * n * v, "head_emit": 4 * n * v, "dh_gemm": 2 * n * v,
-                    "markov_dw2": 2 * n * v}
+                    "markov_dw2": 2 * n * v, "rms_norm_fwd": 6 * n * d}
 
     def cpu_baseline(rows):
         import numpy as np
@@ -401,7 +417,8 @@ def workload_c2m(device, args):
         t_copy = time.perf_counter()
         w32 = weight.float().cpu().numpy()
         w1n, w2n = w1.float().cpu().numpy(), w2.float().cpu().numpy()
-        hs = hidden[:rows].float().cpu().numpy()
+        xs = x[:rows].float().cpu().numpy()
+        wn = norm_w.float().cpu().numpy()
         pv = prev[:rows].cpu().numpy()
         us = teacher[:rows].float().cpu().numpy()
         wt = slots.weights.reshape(-1)[:rows].cpu().numpy()
@@ -409,22 +426,25 @@ def workload_c2m(device, args):
         vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
         t_copy = time.perf_counter() - t_copy
         t0 = time.perf_counter()
+        hs, inv, _ = ref.rms_norm(xs, wn, 1e-6)
         z = ref.lm_head_logits(hs, w32, dtype=np.float32) + ref.markov_logits(pv, w1n, w2n, dtype=np.float32)
         ref.ce_kl_loss(z, us, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
                        dtype=np.float32, chunk_rows=16)
         dl = ref.ce_kl_backward(z, us, wt, y, o.ce, o.kl, 1, dtype=np.float32).astype(np.float32)
-        ref.lm_head_backward(dl, w32, dtype=np.float32)
+        dh = ref.bf16_round(ref.lm_head_backward(dl, w32, dtype=np.float32))
+        ref.rms_norm_backward(dh, xs, inv, wn)
         ref.markov_backward(dl, pv, w1n, w2n, dtype=np.float32)
         dt = time.perf_counter() - t0
         threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
         return dict(value=rows / dt, unit="slots/s", cores=threads, kind="port",
-                    sample=f"numpy fp32 oracle (oracle/objective_ref.py): {rows} of the {n} C2M rows "
-                           f"({rows // 8} whole blocks), d={d}, V={v}, r={r}: LM-head + Markov GEMMs (BLAS, "
-                           f"{threads} threads), ce_kl_loss, ce_kl_backward, dh GEMM, Markov backward; "
-                           f"{dt:.2f} s (weight copy {t_copy:.1f} s untimed)")
+                    sample=f"numpy fp32 oracle (oracle/objective_ref.py): {rows} of the {n} C2X rows "
+                           f"({rows // 8} whole blocks), d={d}, V={v}, r={r}: rms_norm, LM-head + Markov GEMMs "
+                           f"(BLAS, {threads} threads), ce_kl_loss, ce_kl_backward, dh GEMM, rms_norm backward, "
+                           f"Markov backward; {dt:.2f} s (weight copy {t_copy:.1f} s untimed)")
 
-    config = {"workload": "C2M: C2 with the factored Markov head (r=256) fused as a second K segment; "
-                          "fwd, dl + dhidden + markov_w1/w2 grads bwd",
+    config = {"workload": "C2X: C2 with final_norm around the head, the factored Markov head (r=256) fused "
+                          "as a second K segment, and the pooled tail; fwd, dl + dx + final_norm / markov_w1 / "
+                          "markov_w2 grads bwd, gradient factor applied",
               "N": n, "d": d, "V": v, "K": 8, "r": r, "gamma": 4.0, "global_batch": n, "seq_len": None,
               "parallelism": "single GPU"}
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d + 6.0 * v * r,
@@ -434,7 +454,7 @@ def workload_c2m(device, args):
 
 WORKLOADS = {
     "c1": workload_c1,
-    "c2m": workload_c2m,
+    "c2x": workload_c2x,
     "c2": lambda dev, a: workload_head(dev, a, "c2"),
     "c3": lambda dev, a: workload_head(dev, a, "c3"),
     "c4": lambda dev, a: workload_head(dev, a, "c4"),

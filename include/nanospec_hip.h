@@ -11,6 +11,8 @@
  *   nanospec/train.py:276-279 (MarkovHead, layers.py:74-78: embedding + linear)
  *     fused into the LM head as a second K segment -> ns_lmhead_markov_ce_kl_fwd
  *   nanospec/train.py:302-307     dh, markov_w2.grad, markov_w1.grad -> ns_lmhead_markov_bwd
+ *   nanospec/train.py:271, 308-310 final_norm (ops.py:48-66) -> ns_rms_norm_fwd,
+ *                                 ns_rms_norm_bwd, ns_lmhead_norm_bwd (fused after dh)
  *   nanospec/train.py:525-535, shard.py:318-330  pooled metrics, gradient factor
  *                                 -> ns_pooled_tail, ns_scale_gradient
  *
@@ -40,7 +42,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 2
+#define NS_ABI_VERSION 3
 
 #define NS_BF16 0
 #define NS_F32 1
@@ -56,8 +58,25 @@ extern "C" {
 #define NS_WS_LMHEAD 1   /* ns_lmhead_ce_kl_fwd */
 #define NS_WS_LMHEAD_BWD 2 /* ns_lmhead_bwd */
 #define NS_WS_FP8 3      /* ns_fp8_teacher_logits */
+#define NS_WS_RMS_NORM_BWD 4     /* ns_rms_norm_bwd (v ignored) */
+#define NS_WS_LMHEAD_NORM_BWD 5  /* ns_lmhead_norm_bwd */
 
 typedef struct ihipStream_t* ns_stream_t; /* == hipStream_t */
+
+/* Operands of the rms_norm backward (ops.py:55-66) for final_norm (train.py:308-310):
+ * x is the forward's input [N, d] bf16, inv its inverse RMS [N] fp32 (ns_rms_norm_fwd),
+ * weight the norm weight [d] bf16; dx [N, d] bf16 and weight_grad [d] bf16 are written
+ * (weight_grad overwritten, as the reference's copy_).  d % 8 == 0, d <= 16384,
+ * 16-byte aligned base pointers and rows. */
+typedef struct ns_rms_norm_args {
+  const void* x;
+  int64_t ldx;
+  const float* inv;
+  const void* weight;
+  void* dx;
+  int64_t lddx;
+  void* weight_grad;
+} ns_rms_norm_args;
 
 /* Library ABI version (NS_ABI_VERSION); the loader refuses a mismatch. */
 int ns_abi_version(void);
@@ -117,6 +136,25 @@ int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weig
 int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
                   int64_t n, int64_t v, int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream);
 
+/* final_norm forward, ops.rms_norm (ops.py:48-52) at train.py:271:
+ * inv = rsqrt(mean(x^2) + eps) [N] fp32, normalized = bf16(x * inv) (written when not
+ * NULL: the reference's saved activation), out = bf16(weight * normalized).
+ * x, out, normalized [N, d] bf16; weight [d] bf16; d % 8 == 0, d <= 16384. */
+int ns_rms_norm_fwd(const void* x, int64_t ldx, const void* weight, int64_t n, int64_t d, float eps, void* out,
+                    int64_t ldo, void* normalized, int64_t ldn, float* inv, ns_stream_t stream);
+
+/* rms_norm backward alone (ops.py:55-66): dy [N, d] bf16 -> norm->dx, norm->weight_grad.
+ * Workspace NS_WS_RMS_NORM_BWD. */
+int ns_rms_norm_bwd(const void* dy, int64_t lddy, const ns_rms_norm_args* norm, int64_t n, int64_t d, void* workspace,
+                    size_t workspace_bytes, ns_stream_t stream);
+
+/* dh = dl . weight (train.py:302) followed by final_norm's backward (train.py:308-310)
+ * as the split-K reduction of the dh GEMM: dh is never stored unless dh is not NULL.
+ * Workspace NS_WS_LMHEAD_NORM_BWD. */
+int ns_lmhead_norm_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const ns_rms_norm_args* norm,
+                       void* dh, int64_t lddh, int64_t n, int64_t v, int64_t d, void* workspace,
+                       size_t workspace_bytes, ns_stream_t stream);
+
 /* Scratch bytes ns_lmhead_markov_bwd needs for n slots, vocabulary v, hidden d, rank r. */
 size_t ns_lmhead_markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r);
 
@@ -127,11 +165,14 @@ size_t ns_lmhead_markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int
  * d(previous) = dl . w2 comes out of the dh GEMM as extra column tiles (fp32, never
  * rounded); each w1_grad row receives the fp32 sum of its tokens' rows, added in token
  * order (deterministic), rounded once.  Rows whose prev id is outside [0, V) add
- * nothing to w1_grad.  Requires V, d % 8 == 0, r % 64 == 0, n < 2^31. */
+ * nothing to w1_grad.  With norm not NULL, dh feeds final_norm's backward as in
+ * ns_lmhead_norm_bwd (dh may then be NULL).  Requires V, d % 8 == 0, r % 64 == 0,
+ * n < 2^31. */
 int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const int64_t* prev,
                          const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r, void* dh,
-                         int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2, int64_t n, int64_t v,
-                         int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+                         int64_t lddh, const ns_rms_norm_args* norm, void* w1_grad, int64_t ldg1, void* w2_grad,
+                         int64_t ldg2, int64_t n, int64_t v, int64_t d, void* workspace, size_t workspace_bytes,
+                         ns_stream_t stream);
 
 /* Pooled-normalisation tail (train.py:525-535, shard.py:318-327): sums `count` LossMetrics
  * buffers metrics [count][6] in index order (the reference all-reduces numerator,

@@ -18,9 +18,10 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnanospec_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "nanospec_hip.h")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 NS_BF16, NS_F32 = 0, 1
 NS_WS_LOGITS, NS_WS_LMHEAD, NS_WS_LMHEAD_BWD, NS_WS_FP8 = 0, 1, 2, 3
+NS_WS_RMS_NORM_BWD, NS_WS_LMHEAD_NORM_BWD = 4, 5
 
 _c = ctypes
 _P = _c.c_void_p
@@ -28,6 +29,16 @@ _I64 = _c.c_int64
 _F = _c.c_float
 _I = _c.c_int
 _SZ = _c.c_size_t
+
+
+class RmsNormBwd(ctypes.Structure):
+    """struct ns_rms_norm_args of the header."""
+
+    _fields_ = [("x", _P), ("ldx", _I64), ("inv", _P), ("weight", _P), ("dx", _P), ("lddx", _I64),
+                ("weight_grad", _P)]
+
+
+_NORM = ctypes.POINTER(RmsNormBwd)
 
 # argtypes of every exported entry point (kept in the header's order)
 SIGNATURES = {
@@ -53,10 +64,13 @@ SIGNATURES = {
         _I,
     ),
     "ns_lmhead_bwd": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
+    "ns_rms_norm_fwd": ([_P, _I64, _P, _I64, _I64, _F, _P, _I64, _P, _I64, _P, _P], _I),
+    "ns_rms_norm_bwd": ([_P, _I64, _NORM, _I64, _I64, _P, _SZ, _P], _I),
+    "ns_lmhead_norm_bwd": ([_P, _I64, _P, _I64, _NORM, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "ns_lmhead_markov_bwd_workspace_bytes": ([_I64, _I64, _I64, _I64], _SZ),
     "ns_lmhead_markov_bwd": (
-        [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
-         _P, _SZ, _P],
+        [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _NORM, _P, _I64, _P, _I64, _I64, _I64,
+         _I64, _P, _SZ, _P],
         _I,
     ),
     "ns_pooled_tail": ([_P, _I64, _I64, _I64, _P, _P], _I),

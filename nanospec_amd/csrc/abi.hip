@@ -49,6 +49,25 @@ int check_matrix(const void* p, int64_t n, int64_t cols, int64_t ld, const char*
   return NS_OK;
 }
 
+// Validate the rms-norm backward operands and convert them to the internal form.
+int check_norm(const ns_rms_norm_args* nb, int64_t n, int64_t d, ns::NormBwd* out) {
+  if (!nb) return fail(NS_ENULL, "norm is NULL");
+  if (d % 8 || d > ns::kMaxNormD)
+    return fail(NS_EINVAL, "rms-norm hidden size must be a multiple of 8 up to %lld (got %lld)",
+                (long long)ns::kMaxNormD, (long long)d);
+  int rc;
+  if ((rc = check_matrix(nb->x, n, d, nb->ldx, "norm.x"))) return rc;
+  if ((rc = check_matrix(nb->dx, n, d, nb->lddx, "norm.dx"))) return rc;
+  if (n > 0 && (!nb->inv || !nb->weight || !nb->weight_grad))
+    return fail(NS_ENULL, "norm.inv, norm.weight and norm.weight_grad must be non-NULL");
+  if (!aligned(nb->x) || !aligned(nb->dx) || !aligned(nb->weight) || !aligned(nb->weight_grad) || nb->ldx % 8 ||
+      nb->lddx % 8)
+    return fail(NS_EALIGN, "rms-norm operands need 16-byte aligned base pointers and rows");
+  *out = ns::NormBwd{static_cast<const uint16_t*>(nb->x), nb->ldx, nb->inv, static_cast<const uint16_t*>(nb->weight),
+                     static_cast<uint16_t*>(nb->dx), nb->lddx, static_cast<uint16_t*>(nb->weight_grad)};
+  return NS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -68,6 +87,10 @@ size_t ns_workspace_bytes(int kind, int64_t n, int64_t v, int64_t d) {
       return ns::lmhead_bwd_workspace_bytes(n, v, d);
     case NS_WS_FP8:
       return ns::fp8_workspace_bytes(n, d);
+    case NS_WS_RMS_NORM_BWD:
+      return ns::norm_bwd_workspace_bytes(n, d);
+    case NS_WS_LMHEAD_NORM_BWD:
+      return ns::lmhead_bwd_workspace_bytes(n, v, d, 0, true);
     default:
       return 0;
   }
@@ -218,8 +241,9 @@ size_t ns_lmhead_markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int
 
 int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const int64_t* prev,
                          const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r, void* dh,
-                         int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2, int64_t n, int64_t v,
-                         int64_t d, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+                         int64_t lddh, const ns_rms_norm_args* norm, void* w1_grad, int64_t ldg1, void* w2_grad,
+                         int64_t ldg2, int64_t n, int64_t v, int64_t d, void* workspace, size_t workspace_bytes,
+                         ns_stream_t stream) {
   if (n < 0 || n >= (int64_t(1) << 31)) return fail(NS_EINVAL, "n must be in [0, 2^31) (got %lld)", (long long)n);
   if (v < 8 || v % 8 || v >= (int64_t(1) << 31))
     return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 below 2^31 (got %lld)", (long long)v);
@@ -231,20 +255,84 @@ int ns_lmhead_markov_bwd(const void* dl, int64_t ldd, const void* weight, int64_
   if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
   if ((rc = check_matrix(w1, v, r, ldw1, "w1"))) return rc;
   if ((rc = check_matrix(w2, v, r, ldw2, "w2"))) return rc;
-  if ((rc = check_matrix(dh, n, d, lddh, "dh"))) return rc;
+  if ((dh || !norm) && (rc = check_matrix(dh, n, d, lddh, "dh"))) return rc;
+  ns::NormBwd nb{};
+  if (norm && (rc = check_norm(norm, n, d, &nb))) return rc;
   if ((rc = check_matrix(w1_grad, v, r, ldg1, "w1_grad"))) return rc;
   if ((rc = check_matrix(w2_grad, v, r, ldg2, "w2_grad"))) return rc;
   if (!aligned(dl) || !aligned(weight) || !aligned(w1) || !aligned(w2) || !aligned(dh) || !aligned(w1_grad) ||
-      !aligned(w2_grad) || ldd % 8 || ldw % 8 || ldw1 % 8 || ldw2 % 8 || lddh % 4 || ldg1 % 8 || ldg2 % 8)
+      !aligned(w2_grad) || ldd % 8 || ldw % 8 || ldw1 % 8 || ldw2 % 8 || lddh % (norm ? 8 : 4) || ldg1 % 8 ||
+      ldg2 % 8)
     return fail(NS_EALIGN, "Markov backward needs 16-byte aligned base pointers and rows");
   const size_t need = ns::markov_bwd_workspace_bytes(n, v, d, r);
   if (n > 0 && (!workspace || workspace_bytes < need))
     return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
   const ns::MarkovFactors f{prev, w1, w2, ldw1, ldw2, r};
-  return hip_status(ns::markov_backward(dl, ldd, weight, ldw, f, dh, lddh, w1_grad, ldg1, w2_grad, ldg2, n, v, d,
-                                        workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream)),
+  return hip_status(ns::markov_backward(dl, ldd, weight, ldw, f, dh, lddh, norm ? &nb : nullptr, w1_grad, ldg1,
+                                        w2_grad, ldg2, n, v, d, workspace, workspace_bytes,
+                                        reinterpret_cast<hipStream_t>(stream)),
                     "ns_lmhead_markov_bwd");
+}
+
+int ns_rms_norm_fwd(const void* x, int64_t ldx, const void* weight, int64_t n, int64_t d, float eps, void* out,
+                    int64_t ldo, void* normalized, int64_t ldn, float* inv, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (d < 8 || d % 8 || d > ns::kMaxNormD)
+    return fail(NS_EINVAL, "rms-norm hidden size must be a multiple of 8 up to %lld (got %lld)",
+                (long long)ns::kMaxNormD, (long long)d);
+  int rc;
+  if ((rc = check_matrix(x, n, d, ldx, "x"))) return rc;
+  if ((rc = check_matrix(out, n, d, ldo, "out"))) return rc;
+  if (normalized && (rc = check_matrix(normalized, n, d, ldn, "normalized"))) return rc;
+  if (n > 0 && (!weight || !inv)) return fail(NS_ENULL, "weight and inv must be non-NULL");
+  if (!aligned(x) || !aligned(out) || !aligned(weight) || (normalized && !aligned(normalized)) || ldx % 8 || ldo % 8 ||
+      (normalized && ldn % 8))
+    return fail(NS_EALIGN, "rms-norm operands need 16-byte aligned base pointers and rows");
+  return hip_status(ns::rms_norm_forward(x, ldx, weight, n, d, eps, out, ldo, normalized, ldn, inv,
+                                         reinterpret_cast<hipStream_t>(stream)),
+                    "ns_rms_norm_fwd");
+}
+
+int ns_rms_norm_bwd(const void* dy, int64_t lddy, const ns_rms_norm_args* norm, int64_t n, int64_t d, void* workspace,
+                    size_t workspace_bytes, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (d < 8) return fail(NS_EINVAL, "hidden size must be >= 8 (got %lld)", (long long)d);
+  int rc;
+  ns::NormBwd nb{};
+  if ((rc = check_norm(norm, n, d, &nb))) return rc;
+  if ((rc = check_matrix(dy, n, d, lddy, "dy"))) return rc;
+  if (!aligned(dy) || lddy % 8) return fail(NS_EALIGN, "dy needs a 16-byte aligned base pointer and rows");
+  const size_t need = ns::norm_bwd_workspace_bytes(n, d);
+  if (n > 0 && (!workspace || workspace_bytes < need))
+    return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  return hip_status(ns::rms_norm_backward_rows(nullptr, 0, dy, lddy, nb, nullptr, 0, n, d, workspace,
+                                               reinterpret_cast<hipStream_t>(stream)),
+                    "ns_rms_norm_bwd");
+}
+
+int ns_lmhead_norm_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const ns_rms_norm_args* norm,
+                       void* dh, int64_t lddh, int64_t n, int64_t v, int64_t d, void* workspace,
+                       size_t workspace_bytes, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
+  if (d < 8) return fail(NS_EINVAL, "hidden size must be >= 8 (got %lld)", (long long)d);
+  int rc;
+  ns::NormBwd nb{};
+  if ((rc = check_norm(norm, n, d, &nb))) return rc;
+  if ((rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
+  if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
+  if (dh && (rc = check_matrix(dh, n, d, lddh, "dh"))) return rc;
+  if (!aligned(dl) || !aligned(weight) || !aligned(dh) || ldd % 8 || ldw % 8 || (dh && lddh % 8))
+    return fail(NS_EALIGN, "dh GEMM needs 16-byte aligned base pointers and rows");
+  const size_t need = ns::lmhead_bwd_workspace_bytes(n, v, d, 0, true);
+  if (n > 0 && (!workspace || workspace_bytes < need))
+    return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  return hip_status(ns::lmhead_backward_ext(dl, ldd, weight, ldw, nullptr, 0, 0, dh, lddh, nullptr, &nb, n, v, d,
+                                            workspace, reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_norm_bwd");
 }
 
 int ns_pooled_tail(const float* metrics, int64_t count, int64_t world_size, int64_t accumulation_steps, float* out,

@@ -1080,20 +1080,20 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
   return head_forward_typed<float>(p, pl, a, row_stats, metrics, w, st);
 }
 
-size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r) {
+size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r, bool norm) {
   const BwdPlan pl = bwd_plan(n, v, d, r);
   return align_up((size_t)pl.ksplit * n * d * sizeof(float), 256) +
-         align_up((size_t)pl.ksplit2 * n * r * sizeof(float), 256);
+         align_up((size_t)pl.ksplit2 * n * r * sizeof(float), 256) + (norm ? norm_bwd_workspace_bytes(n, d) : 0);
 }
 
 hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
                            int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st) {
-  return lmhead_backward_ext(dl, ldd, weight, ldw, nullptr, 0, 0, dh, lddh, nullptr, n, v, d, ws, st);
+  return lmhead_backward_ext(dl, ldd, weight, ldw, nullptr, 0, 0, dh, lddh, nullptr, nullptr, n, v, d, ws, st);
 }
 
 hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const void* w2,
-                               int64_t ldw2, int64_t r, void* dh, int64_t lddh, float* dprev, int64_t n, int64_t v,
-                               int64_t d, void* ws, hipStream_t st) {
+                               int64_t ldw2, int64_t r, void* dh, int64_t lddh, float* dprev, const NormBwd* norm,
+                               int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st) {
   if (n == 0 || d == 0) return hipSuccess;
   const BwdPlan pl = bwd_plan(n, v, d, r);
   BwdParams p = {};
@@ -1105,7 +1105,10 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
   p.xa = pl.xa; p.xb = pl.xb;
   p.part = static_cast<float*>(ws);
   p.w2 = static_cast<const uint16_t*>(w2); p.ldw2 = ldw2; p.r = r;
-  p.part2 = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)pl.ksplit * n * d * sizeof(float), 256));
+  const size_t b_part = align_up((size_t)pl.ksplit * n * d * sizeof(float), 256);
+  const size_t b_part2 = align_up((size_t)pl.ksplit2 * n * r * sizeof(float), 256);
+  p.part2 = reinterpret_cast<float*>(static_cast<char*>(ws) + b_part);
+  void* norm_ws = static_cast<char*>(ws) + b_part + b_part2;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dh_kernel),
@@ -1119,7 +1122,10 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  {
+  if (norm) {
+    hipError_t e = rms_norm_backward_rows(p.part, pl.ksplit, nullptr, 0, *norm, dh, lddh, n, d, norm_ws, st);
+    if (e != hipSuccess) return e;
+  } else {
     const int64_t quads = (n * d + 3) / 4;
     NS_TIMED("dh_reduce", st);
     hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p.part, pl.ksplit,

@@ -234,7 +234,7 @@ struct MarkovWs {
 };
 
 size_t markov_ws_layout(int64_t n, int64_t v, int64_t d, int64_t r, void* base, MarkovWs* w) {
-  const size_t b_dh = align_up(lmhead_bwd_workspace_bytes(n, v, d, r), 256);
+  const size_t b_dh = align_up(lmhead_bwd_workspace_bytes(n, v, d, r, true), 256);
   const size_t b_dp = align_up((size_t)n * r * sizeof(float), 256);
   const size_t b_e = align_up((size_t)n * r * 2, 256);
   const size_t b_k = align_up((size_t)n * 4, 256);
@@ -261,15 +261,15 @@ size_t markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r) {
 }
 
 hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const MarkovFactors& f,
-                           void* dh, int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2,
-                           int64_t n, int64_t v, int64_t d, void* ws, size_t ws_bytes, hipStream_t st) {
+                           void* dh, int64_t lddh, const NormBwd* norm, void* w1_grad, int64_t ldg1, void* w2_grad,
+                           int64_t ldg2, int64_t n, int64_t v, int64_t d, void* ws, size_t ws_bytes, hipStream_t st) {
   const int64_t r = f.r;
   MarkovWs w;
   markov_ws_layout(n, v, d, r, ws, &w);
   hipError_t e;
-  // dh and d(previous) in one GEMM
-  if ((e = lmhead_backward_ext(dl, ldd, weight, ldw, f.w2, f.ldw2, r, dh, lddh, w.dprev, n, v, d, w.dh_ws, st)) !=
-      hipSuccess)
+  // dh (or the rms-norm backward) and d(previous) in one GEMM
+  if ((e = lmhead_backward_ext(dl, ldd, weight, ldw, f.w2, f.ldw2, r, dh, lddh, w.dprev, norm, n, v, d, w.dh_ws,
+                               st)) != hipSuccess)
     return e;
   if (n == 0) return hipSuccess;
   {

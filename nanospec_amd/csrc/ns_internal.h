@@ -38,6 +38,28 @@ hipError_t launch_merge(const RowPart* part1, const float* zy, int64_t v, int sp
 hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, float* row_stats,
                            float* metrics, hipStream_t st);
 
+// ---- final_norm around the head (norm.hip) ------------------------------------
+constexpr int64_t kMaxNormD = 16384;   // hidden sizes the rms-norm kernels hold in registers
+// rms_norm backward operands (ops.py:55-66): x the forward's input, inv its [N] inverse
+// RMS, w the norm weight [d]; outputs dx [N, d] and wgrad [d] (overwritten), all bf16
+struct NormBwd {
+  const uint16_t* x;
+  int64_t ldx;
+  const float* inv;
+  const uint16_t* w;
+  uint16_t* dx;
+  int64_t lddx;
+  uint16_t* wgrad;
+};
+int norm_rows_per_block(int64_t n);
+size_t norm_bwd_workspace_bytes(int64_t n, int64_t d);
+hipError_t rms_norm_forward(const void* x, int64_t ldx, const void* weight, int64_t n, int64_t d, float eps,
+                            void* out, int64_t ldo, void* normalized, int64_t ldn, float* inv, hipStream_t st);
+// dy from split-K partials part[ksplit][N][d] (dh_out, if not NULL, receives bf16 dh) or,
+// with part == NULL, from the bf16 tensor dy
+hipError_t rms_norm_backward_rows(const float* part, int ksplit, const void* dy, int64_t lddy, const NormBwd& nb,
+                                  void* dh_out, int64_t lddh, int64_t n, int64_t d, void* ws, hipStream_t st);
+
 // ---- fused LM-head path (lmhead.hip) ---------------------------------------
 // Markov head in factored form: logits += W1[prev] . W2^T (rank r, r % 64 == 0).
 struct MarkovFactors {
@@ -51,20 +73,24 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
                           const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
                           int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd,
                           float* row_stats, float* metrics, void* ws, hipStream_t st);
-// dh workspace; r > 0 adds the Markov column tiles' partials
-size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r = 0);
+// dh workspace; r > 0 adds the Markov column tiles' partials, norm the rms-norm
+// backward's column partials
+size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r = 0, bool norm = false);
 hipError_t lmhead_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh,
                            int64_t lddh, int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st);
-// dh = dl . weight and, when r > 0, dprev = dl . w2 (fp32 [N, r], row stride r) in the same GEMM
+// dh = dl . weight and, when r > 0, dprev = dl . w2 (fp32 [N, r], row stride r) in the same
+// GEMM.  With norm, the split-K reduction is the rms-norm backward: dx and the norm weight's
+// gradient are written, and dh only if dh is not NULL.
 hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const void* w2,
-                               int64_t ldw2, int64_t r, void* dh, int64_t lddh, float* dprev, int64_t n, int64_t v,
-                               int64_t d, void* ws, hipStream_t st);
-// Markov-head backward (markov.hip): dh, w2_grad = dl^T . w1[prev] (overwritten) and
-// w1_grad.index_add_(prev, dl . w2) (accumulated, deterministic order)
+                               int64_t ldw2, int64_t r, void* dh, int64_t lddh, float* dprev, const NormBwd* norm,
+                               int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st);
+// Markov-head backward (markov.hip): dh (or, with norm, dx and the norm weight's gradient),
+// w2_grad = dl^T . w1[prev] (overwritten) and w1_grad.index_add_(prev, dl . w2)
+// (accumulated, deterministic order)
 size_t markov_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r);
 hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int64_t ldw, const MarkovFactors& f,
-                           void* dh, int64_t lddh, void* w1_grad, int64_t ldg1, void* w2_grad, int64_t ldg2,
-                           int64_t n, int64_t v, int64_t d, void* ws, size_t ws_bytes, hipStream_t st);
+                           void* dh, int64_t lddh, const NormBwd* norm, void* w1_grad, int64_t ldg1, void* w2_grad,
+                           int64_t ldg2, int64_t n, int64_t v, int64_t d, void* ws, size_t ws_bytes, hipStream_t st);
 hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                          int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d,
                          hipStream_t st);

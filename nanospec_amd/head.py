@@ -18,6 +18,7 @@ which feeds the dh = dl . W GEMM in the backward.  The metrics keep the
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -153,14 +154,48 @@ def _grad_rows(t: torch.Tensor, vocab: int, r: int, name: str):
     return t, t.stride(0)
 
 
+def _final_norm_args(final_norm, n, d, device):
+    """(struct pointer, dx, keep-alive) for final_norm = (RMSActivations, weight, weight_grad)."""
+    from nanospec_amd import ops
+
+    saved, weight, weight_grad = final_norm
+    if saved.input.shape[-1] != d or saved.input.numel() // d != n:
+        raise ValueError(f"final_norm input {tuple(saved.input.shape)} does not match dh [{n}, {d}]")
+    _lib.require_device(saved.input, weight, weight_grad)
+    dx = torch.empty((n, d), dtype=torch.bfloat16, device=device)
+    args, keep = ops.norm_args(saved, weight, weight_grad, dx)
+    return ctypes.byref(args), dx, (args, keep)
+
+
 @torch.no_grad()
-def lm_head_markov_backward(dl, lm_head_weight, markov: MarkovFactors, w1_grad, w2_grad):
+def lm_head_norm_backward(dl, lm_head_weight, final_norm):
+    """dh = dl . W_lm (train.py:302) followed by final_norm's backward (train.py:308-310,
+    ops.py:55-66) as the dh GEMM's split-K reduction: returns dx [..., d] bf16 and
+    overwrites the norm weight's gradient; dh is never stored.  final_norm =
+    (RMSActivations from ops.rms_norm, norm weight, norm weight gradient buffer)."""
+    vocab, d = lm_head_weight.shape
+    device = _lib.require_device(dl, lm_head_weight)
+    g, ldg = _bf16_rows(dl, vocab, "dl")
+    w, ldw = _bf16_rows(lm_head_weight, d, "lm_head_weight")
+    n = g.shape[0]
+    args, dx, keep = _final_norm_args(final_norm, n, d, device)
+    ws = _lib.workspace(_lib.NS_WS_LMHEAD_NORM_BWD, n, vocab, d, device)
+    status = _lib.load().ns_lmhead_norm_bwd(_lib.ptr(g), ldg, _lib.ptr(w), ldw, args, None, d, n, vocab, d,
+                                            _lib.ptr(ws), ws.numel(), _lib.stream(device))
+    _lib.check(status, "ns_lmhead_norm_bwd")
+    del keep
+    return dx.view(final_norm[0].input.shape)
+
+
+@torch.no_grad()
+def lm_head_markov_backward(dl, lm_head_weight, markov: MarkovFactors, w1_grad, w2_grad, final_norm=None):
     """The head backward with the factored Markov head (train.py:302-307):
     dh = dl . W_lm; markov_w2.grad = dl^T . w1[previous] (overwritten, as
     ops.linear_backward's copy_, ops.py:38-45); markov_w1.grad.index_add_(previous,
     dl . w2) (accumulated, ops.embedding_backward, ops.py:73-74).  d(previous) stays
     fp32 inside the library and each w1.grad row gets its tokens' sum in token order.
-    Returns dh [..., d] bf16."""
+    Returns dh [..., d] bf16, or with ``final_norm`` (as in ``lm_head_norm_backward``)
+    dx [..., d] bf16."""
     vocab, d = lm_head_weight.shape
     device = _lib.require_device(dl, lm_head_weight, markov.w1, markov.w2, w1_grad, w2_grad)
     g, ldg = _bf16_rows(dl, vocab, "dl")
@@ -170,25 +205,33 @@ def lm_head_markov_backward(dl, lm_head_weight, markov: MarkovFactors, w1_grad, 
     g1, ldg1 = _grad_rows(w1_grad, vocab, r, "w1_grad")
     g2, ldg2 = _grad_rows(w2_grad, vocab, r, "w2_grad")
     lib = _lib.load()
-    dh = torch.empty((n, d), dtype=torch.bfloat16, device=device)
+    if final_norm is not None:
+        args, out, keep = _final_norm_args(final_norm, n, d, device)
+        dh = None
+    else:
+        args, keep = None, None
+        out = dh = torch.empty((n, d), dtype=torch.bfloat16, device=device)
     nbytes = int(lib.ns_lmhead_markov_bwd_workspace_bytes(n, vocab, d, r))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
     status = lib.ns_lmhead_markov_bwd(
         _lib.ptr(g), ldg, _lib.ptr(w), ldw, _lib.ptr(prev), _lib.ptr(w1), ldw1, _lib.ptr(w2), ldw2, r,
-        _lib.ptr(dh), d, _lib.ptr(g1), ldg1, _lib.ptr(g2), ldg2, n, vocab, d, _lib.ptr(ws), ws.numel(),
+        _lib.ptr(dh), d, args, _lib.ptr(g1), ldg1, _lib.ptr(g2), ldg2, n, vocab, d, _lib.ptr(ws), ws.numel(),
         _lib.stream(device),
     )
     _lib.check(status, "ns_lmhead_markov_bwd")
-    return dh.view(tuple(dl.shape[:-1]) + (d,))
+    del keep
+    return out.view(tuple(dl.shape[:-1]) + (d,))
 
 
 @torch.no_grad()
 def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, return_dlogits=False,
-                           markov_grads=None):
+                           markov_grads=None, final_norm=None):
     """dh = dl . W_lm with the dl emitted by the forward.  Returns dh [..., d] bf16
     (and dl [..., V] bf16 when ``return_dlogits``, for the Markov backward).
     ``markov_grads=(w1_grad, w2_grad)`` with a factored Markov forward also runs the
-    Markov-head backward in the same GEMM (``lm_head_markov_backward``)."""
+    Markov-head backward in the same GEMM (``lm_head_markov_backward``).
+    ``final_norm=(RMSActivations, norm weight, norm weight grad)`` fuses final_norm's
+    backward into the dh reduction and returns dx in place of dh (train.py:308-310)."""
     if saved.dlogits is None:
         raise ValueError("no dl to propagate: the forward ran with emit_dlogits=False, or the backward already ran")
     if accumulation_steps != saved.accumulation_steps:
@@ -200,7 +243,9 @@ def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, retu
     if markov_grads is not None:
         if saved.markov is None:
             raise ValueError("markov_grads given, but the forward ran without Markov factors")
-        dh = lm_head_markov_backward(dl, saved.weight, saved.markov, *markov_grads)
+        dh = lm_head_markov_backward(dl, saved.weight, saved.markov, *markov_grads, final_norm=final_norm)
+    elif final_norm is not None:
+        dh = lm_head_norm_backward(dl, saved.weight, final_norm)
     else:
         dh = lm_head_linear_backward(dl, saved.weight)
     dl = dl.view(saved.shape)

@@ -26,6 +26,10 @@ markov_logits / backward   torch F.embedding + F.linear forward, torch.autograd
                            for d(previous), d(w2) and the index_add d(w1);
                            hand-worked index_add with repeated ids
 slot_preparation           hand-computed known answers; brute-force loops
+rms_norm                   fp64 closed form x / sqrt(mean(x^2) + eps)
+rms_norm_backward          torch.autograd (fp64) of sum(dy * weight * rms_norm(x))
+                           for dx and the weight gradient, with dy correlated with
+                           x so the projection (dvar) term carries weight
 pooled_tail                hand-computed known answers (den = 0 -> factor 0 and
                            the 1e-6 clamp; accept total 0 -> clamp 1); torch's
                            own evaluation of shard.py:321-327 on fp32 tensors;
@@ -326,6 +330,47 @@ def markov_backward(dl, prev, w1, w2, dtype=np.float64):
     dw1 = np.zeros(np.shape(w1), dtype=dtype)
     np.add.at(dw1, prev, dprev)
     return dprev, dw2, dw1
+
+
+# ---------------------------------------------------------------------------
+# final_norm  ops.py:48-66 (train.py:271, 308-310)
+# ---------------------------------------------------------------------------
+
+
+def rms_norm(x, weight, eps):
+    """ops.rms_norm (ops.py:48-52) in fp32 with the rounding points of torch's device
+    kernels: mean = sum(x*x) * (1/d), inv = 1/sqrt(mean + eps), normalized = bf16(x * inv),
+    out = bf16(weight * normalized).  x and weight hold bf16 values.  Returns
+    (out, inv [N], normalized)."""
+    x = np.asarray(x, dtype=np.float32)
+    w = np.asarray(weight, dtype=np.float32)
+    d = x.shape[-1]
+    sq = (x * x).astype(np.float32)
+    mean = (sq.sum(-1, dtype=np.float32) * np.float32(1.0 / np.float32(d))).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt((mean + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    normalized = bf16_round(x * inv[..., None])
+    out = bf16_round(w * normalized)
+    return out, inv, normalized
+
+
+def rms_norm_backward(dy, x, inv, weight):
+    """ops.rms_norm_backward (ops.py:55-66) in fp32: dw = bf16(sum_rows bf16(dy * normalized)),
+    dz = bf16(dy * weight), dinv = sum(dz * x), dvar = dinv * (-0.5 * inv^3),
+    dx = bf16(dz * inv + (dvar * (1/d)) * (2 x)).  torch divides by the host scalar d through
+    its reciprocal on the device, kept here.  Returns (dx, dw)."""
+    dy = np.asarray(dy, dtype=np.float32)
+    x = np.asarray(x, dtype=np.float32)
+    w = np.asarray(weight, dtype=np.float32)
+    inv = np.asarray(inv, dtype=np.float32).reshape(-1, 1)
+    d = x.shape[-1]
+    normalized = bf16_round(x * inv)
+    dw = bf16_round(bf16_round(dy * normalized).sum(0, dtype=np.float32))
+    dz = bf16_round(dy * w)
+    dinv = (dz * x).astype(np.float32).sum(-1, keepdims=True, dtype=np.float32)
+    dvar = (dinv * (np.float32(-0.5) * ((inv * inv) * inv))).astype(np.float32)
+    q = (dvar * np.float32(np.float32(1.0) / np.float32(d))).astype(np.float32)
+    dx = bf16_round((dz * inv).astype(np.float32) + (q * (np.float32(2.0) * x)).astype(np.float32))
+    return dx, dw
 
 
 # ---------------------------------------------------------------------------

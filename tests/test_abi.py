@@ -65,3 +65,44 @@ def test_status_mapping(lib):
     _fwd(lib, zdt=9)
     with pytest.raises(ValueError, match="dtype"):
         _lib.check(-2, "ns_ce_kl_logits_fwd")
+
+
+def _norm_args(**over):
+    a = dict(x=256, ldx=64, inv=256, weight=256, dx=512, lddx=64, weight_grad=768)
+    a.update(over)
+    return _lib.RmsNormBwd(a["x"], a["ldx"], a["inv"], a["weight"], a["dx"], a["lddx"], a["weight_grad"])
+
+
+@pytest.mark.parametrize("over,d,code,text", [
+    (dict(), 60, -1, "multiple of 8"),
+    (dict(), 16392, -1, "up to 16384"),
+    (dict(ldx=32), 64, -1, "leading dimension"),
+    (dict(inv=None), 64, -5, "non-NULL"),
+    (dict(dx=520), 64, -3, "aligned"),
+    (dict(), 64, -4, "workspace"),
+])
+def test_rms_norm_bwd_validation(lib, over, d, code, text):
+    args = _norm_args(**over)
+    rc = lib.ns_rms_norm_bwd(ctypes.c_void_p(256), d, ctypes.byref(args), 4, d, None, 0, None)
+    assert rc == code
+    assert text in lib.ns_last_error().decode()
+
+
+def test_markov_and_pooled_validation(lib):
+    p = ctypes.c_void_p
+    # rank not a multiple of 64
+    rc = lib.ns_lmhead_markov_bwd(p(256), 64, p(256), 64, p(256), p(256), 64, p(256), 64, 32, p(256), 64, None,
+                                  p(256), 64, p(256), 64, 8, 64, 64, p(256), 1 << 20, None)
+    assert rc == -1 and "Markov rank" in lib.ns_last_error().decode()
+    # dh may be NULL only with a norm
+    rc = lib.ns_lmhead_markov_bwd(p(256), 64, p(256), 64, p(256), p(256), 64, p(256), 64, 64, None, 64, None,
+                                  p(256), 64, p(256), 64, 8, 64, 64, p(256), 1 << 20, None)
+    assert rc == -5 and "dh is NULL" in lib.ns_last_error().decode()
+    assert lib.ns_pooled_tail(p(256), 0, 1, 1, p(256), None) == -1
+    assert lib.ns_pooled_tail(p(256), 1, 0, 1, p(256), None) == -1
+    assert lib.ns_scale_gradient(p(256), 5, 8, p(256), None) == -2
+    assert lib.ns_scale_gradient(p(260), 0, 8, p(256), None) == -3
+    assert lib.ns_lmhead_markov_bwd_workspace_bytes(4096, 248320, 5120, 256) > \
+        lib.ns_workspace_bytes(_lib.NS_WS_LMHEAD_BWD, 4096, 248320, 5120)
+    assert lib.ns_workspace_bytes(_lib.NS_WS_LMHEAD_NORM_BWD, 4096, 248320, 5120) > \
+        lib.ns_workspace_bytes(_lib.NS_WS_LMHEAD_BWD, 4096, 248320, 5120)

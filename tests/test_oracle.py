@@ -395,3 +395,52 @@ def test_scale_gradient_matches_torch_mul(dtype):
         want = g.clone().mul_(factor.to(dtype)).float().numpy()
         got = ref.scale_gradient(g.float().numpy(), factor.item(), bf16=dtype == torch.bfloat16)
         assert np.array_equal(got, want), f
+
+
+# --------------------------------------------------------------- final_norm
+
+
+def _norm_case(n, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = (2.0 * torch.randn(n, d, generator=g) + 0.5).bfloat16()
+    w = (1.0 + 0.1 * torch.randn(d, generator=g)).bfloat16()
+    return x.float().numpy(), w.float().numpy(), g
+
+
+@pytest.mark.parametrize("n,d", [(7, 64), (33, 320)])
+def test_rms_norm_matches_closed_form(n, d):
+    x, w, _ = _norm_case(n, d, 3)
+    eps = 1e-6
+    out, inv, normalized = ref.rms_norm(x, w, eps)
+    x64 = x.astype(np.float64)
+    inv64 = 1.0 / np.sqrt((x64 ** 2).mean(-1) + eps)
+    assert np.all(np.abs(inv - inv64) <= 4 * np.spacing(inv.astype(np.float32)))
+    exact_n = x64 * inv64[:, None]
+    assert np.all(np.abs(normalized - exact_n) <= np.abs(exact_n) * 2.0 ** -8 + 1e-30)
+    exact_o = w.astype(np.float64) * exact_n
+    assert np.all(np.abs(out - exact_o) <= np.abs(exact_o) * 2.0 ** -7 + 1e-30)
+    # torch's own rms_norm (fp64) agrees with the closed form
+    t = F.rms_norm(torch.from_numpy(x64), (d,), torch.from_numpy(w.astype(np.float64)), eps)
+    np.testing.assert_allclose(t.numpy(), w * exact_n, rtol=1e-12)
+
+
+@pytest.mark.parametrize("n,d", [(9, 64), (40, 320)])
+def test_rms_norm_backward_matches_autograd(n, d):
+    x, w, g = _norm_case(n, d, 4)
+    eps = 1e-6
+    _, inv, normalized = ref.rms_norm(x, w, eps)
+    # dy correlated with the normalized input: the projection term is O(1) of dx
+    dy = torch.from_numpy(normalized * w).clone()
+    dy = (dy * 0.7 + 0.3 * torch.randn(n, d, generator=g)).bfloat16().float().numpy()
+    dx, dw = ref.rms_norm_backward(dy, x, inv, w)
+    tx = torch.from_numpy(x.astype(np.float64)).requires_grad_()
+    tw = torch.from_numpy(w.astype(np.float64)).requires_grad_()
+    y = tw * (tx * torch.rsqrt(tx.pow(2).mean(-1, keepdim=True) + eps))
+    (y * torch.from_numpy(dy.astype(np.float64))).sum().backward()
+    sim = ref.similarity(dx, tx.grad.numpy())
+    assert sim["cosine_min"] >= 0.9999 and sim["relative_l2"] <= 5e-3, sim
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=2e-2, atol=2e-2 * np.abs(tw.grad.numpy()).max())
+    # a planted mistake (the dvar term dropped) is caught by the same bar
+    dz = ref.bf16_round(dy * w)
+    wrong = ref.bf16_round(dz * inv[:, None])
+    assert ref.similarity(wrong, tx.grad.numpy())["cosine_min"] < 0.9999
