@@ -70,6 +70,7 @@ KERNEL_NAMES = [
     # stream_emit_kernel<TZ, TU, TD, VEC, EMIT, ACCEPT>
     (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), true", "stream_emit"),
     (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), false", "stream_accept"),
+    (r"lse_merge_kernel", "lse_merge"),
     (r"merge_kernel", "merge_rows"),
     (r"finalize_kernel", "finalize_metrics"),
     (r"accept_rows_kernel", "accept_rows"),
@@ -293,8 +294,9 @@ def workload_head(device, args, which):
     def step():
         u = teacher
         if fp8 is not None:
+            # the fp8 head also forms each teacher row's log-sum-exp, so pass 1 reads no teacher
             xt, codes, scale = fp8
-            u = ops.fp8_linear(xt, codes.view(torch.float8_e4m3fn), scale)
+            u = ops.fp8_teacher_logits(xt, codes.view(torch.float8_e4m3fn), scale)
         metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, u, slots, o, markov_logits=markov)
         dh = head.lm_head_ce_kl_backward(saved)
         return metrics, dh

@@ -11,6 +11,8 @@
  *   nanospec/train.py:276-279 (MarkovHead, layers.py:74-78: embedding + linear)
  *     fused into the LM head as a second K segment -> ns_lmhead_markov_ce_kl_fwd
  *   nanospec/train.py:302-307     dh, markov_w2.grad, markov_w1.grad -> ns_lmhead_markov_bwd
+ *   nanospec/train.py:172-173, 280-290  teacher logits (producer LSE, gathered rows)
+ *                                 -> ns_lmhead_teacher_logits, ns_teacher_args
  *   nanospec/train.py:271, 308-310 final_norm (ops.py:48-66) -> ns_rms_norm_fwd,
  *                                 ns_rms_norm_bwd, ns_lmhead_norm_bwd (fused after dh)
  *   nanospec/train.py:525-535, shard.py:318-330  pooled metrics, gradient factor
@@ -42,7 +44,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 3
+#define NS_ABI_VERSION 4
 
 #define NS_BF16 0
 #define NS_F32 1
@@ -60,6 +62,7 @@ extern "C" {
 #define NS_WS_FP8 3      /* ns_fp8_teacher_logits */
 #define NS_WS_RMS_NORM_BWD 4     /* ns_rms_norm_bwd (v ignored) */
 #define NS_WS_LMHEAD_NORM_BWD 5  /* ns_lmhead_norm_bwd */
+#define NS_WS_TEACHER_LOGITS 6   /* ns_lmhead_teacher_logits with lse (d ignored) */
 
 typedef struct ihipStream_t* ns_stream_t; /* == hipStream_t */
 
@@ -68,6 +71,18 @@ typedef struct ihipStream_t* ns_stream_t; /* == hipStream_t */
  * weight the norm weight [d] bf16; dx [N, d] bf16 and weight_grad [d] bf16 are written
  * (weight_grad overwritten, as the reference's copy_).  d % 8 == 0, d <= 16384,
  * 16-byte aligned base pointers and rows. */
+/* Teacher logits as their producer left them (train.py:280-290).  Objective row t reads
+ * row rows[t] of the teacher tensor, which has n_rows rows (rows NULL: row t, and n_rows
+ * is n or 0): the gather of train.py:285-290 (teacher_indices, dspark.py:143) happens in
+ * the load, with no gathered copy.  An index outside [0, n_rows) makes that row NaN.
+ * lse, when not NULL, is the log-sum-exp of every teacher row (ns_lmhead_teacher_logits
+ * writes it): the first pass then reads no teacher logits and the second forms KL. */
+typedef struct ns_teacher_args {
+  const int64_t* rows;
+  int64_t n_rows;
+  const float* lse;
+} ns_teacher_args;
+
 typedef struct ns_rms_norm_args {
   const void* x;
   int64_t ldx;
@@ -85,7 +100,7 @@ int ns_abi_version(void);
 const char* ns_last_error(void);
 
 /* Scratch bytes an entry point of `kind` needs (NS_WS_*); d is ignored by
- * NS_WS_LOGITS, v by NS_WS_FP8. */
+ * NS_WS_LOGITS and NS_WS_TEACHER_LOGITS, v by NS_WS_RMS_NORM_BWD. */
 size_t ns_workspace_bytes(int kind, int64_t n, int64_t v, int64_t d);
 
 /* Forward objective over given logits (objective.py:49-67) plus, when dl is not
@@ -113,10 +128,11 @@ int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, 
  * or NULL, teacher [N, V] (t_dtype), dl [N, V] bf16 or NULL.
  * Requires d % 64 == 0, V % 8 == 0, 16-byte aligned rows, n % k == 0. */
 int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
-                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
-                        const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
-                        float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
-                        float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
+                        const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,
+                        const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k, float c_ce, float c_kl,
+                        float inv_acc, void* dl, int64_t ldd, float* row_stats, float* metrics, void* workspace,
+                        size_t workspace_bytes, ns_stream_t stream);
 
 /* The same forward with the Markov head in factored form (train.py:276-279):
  * z = hidden . weight^T + w1[prev] . w2^T, formed as one GEMM with K = d + r
@@ -126,10 +142,21 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
  * NaN (the reference's embedding lookup raises). */
 int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const int64_t* prev,
                                const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r,
-                               const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
-                               const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
-                               float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
-                               float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream);
+                               const void* teacher, int t_dtype, int64_t ldt, const ns_teacher_args* teacher_args,
+                               const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n,
+                               int64_t d, int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl,
+                               int64_t ldd, float* row_stats, float* metrics, void* workspace,
+                               size_t workspace_bytes, ns_stream_t stream);
+
+/* Teacher-logit producer (train.py:172-173 and 281-284: ops.linear of the teacher's last
+ * hidden state, gathered at teacher_indices, by the shared LM head):
+ * out[t] = bf16(x[rows[t]] . weight^T), rows NULL: x[t].  When lse is not NULL, lse[t] =
+ * log-sum-exp of out's bf16 row t, formed in the GEMM epilogue (workspace
+ * NS_WS_TEACHER_LOGITS), for ns_teacher_args.lse.  x [n_rows, d] bf16 (d % 64 == 0),
+ * out [n, V] bf16. */
+int ns_lmhead_teacher_logits(const void* x, int64_t ldx, const int64_t* rows, int64_t n_rows, const void* weight,
+                             int64_t ldw, void* out, int64_t ldo, float* lse, int64_t n, int64_t v, int64_t d,
+                             void* workspace, size_t workspace_bytes, ns_stream_t stream);
 
 /* LM-head backward dh = dl . weight (train.py:302): dl [N, V] bf16, weight [V, d]
  * bf16, dh [N, d] bf16.  Split-K over V with a fixed-order fp32 reduction. */
@@ -196,9 +223,11 @@ int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw
  * even), wq [V, d] holds e4m3 codes with one fp32 scale per 128x128 block in
  * scale [V/128, d/128] (the scale multiplies); out [N, V] bf16 = bf16 of the fp32
  * sum over K blocks of x_scale * w_scale * (fp8 dot product on MFMA).
+ * lse, when not NULL, receives the log-sum-exp of each bf16 output row [N] fp32, formed in
+ * the GEMM epilogue, for ns_teacher_args.lse.
  * Requires V % 128 == 0 and d % 128 == 0 (ValueError in the reference). */
 int ns_fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const float* scale,
-                          void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, void* workspace,
+                          void* out, int64_t ldo, float* lse, int64_t n, int64_t v, int64_t d, void* workspace,
                           size_t workspace_bytes, ns_stream_t stream);
 
 /* The activation half of the above alone: q [N, d] e4m3 codes (row stride d) and

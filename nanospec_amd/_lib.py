@@ -18,10 +18,10 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnanospec_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "nanospec_hip.h")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 NS_BF16, NS_F32 = 0, 1
 NS_WS_LOGITS, NS_WS_LMHEAD, NS_WS_LMHEAD_BWD, NS_WS_FP8 = 0, 1, 2, 3
-NS_WS_RMS_NORM_BWD, NS_WS_LMHEAD_NORM_BWD = 4, 5
+NS_WS_RMS_NORM_BWD, NS_WS_LMHEAD_NORM_BWD, NS_WS_TEACHER_LOGITS = 4, 5, 6
 
 _c = ctypes
 _P = _c.c_void_p
@@ -40,6 +40,15 @@ class RmsNormBwd(ctypes.Structure):
 
 _NORM = ctypes.POINTER(RmsNormBwd)
 
+
+class TeacherArgs(ctypes.Structure):
+    """struct ns_teacher_args of the header."""
+
+    _fields_ = [("rows", _P), ("n_rows", _I64), ("lse", _P)]
+
+
+_TEACH = ctypes.POINTER(TeacherArgs)
+
 # argtypes of every exported entry point (kept in the header's order)
 SIGNATURES = {
     "ns_abi_version": ([], _I),
@@ -54,13 +63,17 @@ SIGNATURES = {
         _I,
     ),
     "ns_lmhead_ce_kl_fwd": (
-        [_P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F,
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _TEACH, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F,
          _P, _I64, _P, _P, _P, _SZ, _P],
         _I,
     ),
     "ns_lmhead_markov_ce_kl_fwd": (
-        [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I, _I64, _P, _P, _P, _I64, _I64, _I64, _I64,
-         _F, _F, _F, _P, _I64, _P, _P, _P, _SZ, _P],
+        [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I, _I64, _TEACH, _P, _P, _P, _I64, _I64, _I64,
+         _I64, _F, _F, _F, _P, _I64, _P, _P, _P, _SZ, _P],
+        _I,
+    ),
+    "ns_lmhead_teacher_logits": (
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P],
         _I,
     ),
     "ns_lmhead_bwd": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
@@ -76,7 +89,7 @@ SIGNATURES = {
     "ns_pooled_tail": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ns_scale_gradient": ([_P, _I, _I64, _P, _P], _I),
     "ns_lmhead_linear": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], _I),
-    "ns_fp8_teacher_logits": ([_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
+    "ns_fp8_teacher_logits": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "ns_fp8_quantize_rows": ([_P, _I64, _I64, _I64, _P, _P, _P], _I),
     "ns_prepare_slots": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _P], _I),
 }

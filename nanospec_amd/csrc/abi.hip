@@ -86,11 +86,13 @@ size_t ns_workspace_bytes(int kind, int64_t n, int64_t v, int64_t d) {
     case NS_WS_LMHEAD_BWD:
       return ns::lmhead_bwd_workspace_bytes(n, v, d);
     case NS_WS_FP8:
-      return ns::fp8_workspace_bytes(n, d);
+      return ns::fp8_workspace_bytes(n, v, d);
     case NS_WS_RMS_NORM_BWD:
       return ns::norm_bwd_workspace_bytes(n, d);
     case NS_WS_LMHEAD_NORM_BWD:
       return ns::lmhead_bwd_workspace_bytes(n, v, d, 0, true);
+    case NS_WS_TEACHER_LOGITS:
+      return ns::lmhead_linear_lse_workspace_bytes(n, v);
     default:
       return 0;
   }
@@ -147,7 +149,7 @@ namespace {
 // Shared validation and launch of the fused forward (dense Markov addend or factors).
 int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
                        int64_t ldm, const ns::MarkovFactors* factors, const void* teacher, int t_dtype, int64_t ldt,
-                       const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n, int64_t d,
+                       const ns_teacher_args* targs, const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n, int64_t d,
                        int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd,
                        float* row_stats, float* metrics, void* workspace, size_t workspace_bytes,
                        ns_stream_t stream, const char* name) {
@@ -159,7 +161,13 @@ int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int6
   if ((rc = check_matrix(hidden, n, d, ldh, "hidden"))) return rc;
   if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
   if (markov && (rc = check_matrix(markov, n, v, ldm, "markov"))) return rc;
-  if ((rc = check_matrix(teacher, n, v, ldt, "teacher"))) return rc;
+  // with teacher rows, the teacher tensor has its own row count (train.py:285-290 gathers it)
+  const int64_t nt = targs && targs->rows ? targs->n_rows : n;
+  if (targs && targs->rows && (nt < 1 || nt >= (int64_t(1) << 31)))
+    return fail(NS_EINVAL, "teacher n_rows must be in [1, 2^31) (got %lld)", (long long)nt);
+  if (targs && n > 0 && targs->n_rows > 0 && !targs->rows && targs->n_rows != n)
+    return fail(NS_EINVAL, "teacher n_rows %lld without rows must equal n", (long long)targs->n_rows);
+  if ((rc = check_matrix(teacher, nt, v, ldt, "teacher"))) return rc;
   if (dl && (rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
   if (!metrics || (n > 0 && !row_stats)) return fail(NS_ENULL, "metrics and row_stats must be non-NULL");
   const int64_t tq = t_dtype == NS_BF16 ? 8 : 4;
@@ -183,8 +191,10 @@ int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int6
     return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
   ns::SlotArgs a{labels, weights, valid, n, k, c_ce, c_kl, inv_acc};
+  const ns::TeacherSpec ts{targs ? targs->rows : nullptr, nt, targs ? targs->lse : nullptr};
   return hip_status(ns::lmhead_forward(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, d, v,
-                                       a, dl, ldd, row_stats, metrics, workspace, reinterpret_cast<hipStream_t>(stream)),
+                                       a, &ts, dl, ldd, row_stats, metrics, workspace,
+                                       reinterpret_cast<hipStream_t>(stream)),
                     name);
 }
 
@@ -193,25 +203,59 @@ int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int6
 extern "C" {
 
 int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
-                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
-                        const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
-                        float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
-                        float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
-  return lmhead_fwd_checked(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, labels, weights,
-                            valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, workspace,
-                            workspace_bytes, stream, "ns_lmhead_ce_kl_fwd");
+                        int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
+                        const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,
+                        const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k, float c_ce, float c_kl,
+                        float inv_acc, void* dl, int64_t ldd, float* row_stats, float* metrics, void* workspace,
+                        size_t workspace_bytes, ns_stream_t stream) {
+  return lmhead_fwd_checked(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, teacher_args,
+                            labels, weights, valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics,
+                            workspace, workspace_bytes, stream, "ns_lmhead_ce_kl_fwd");
 }
 
 int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const int64_t* prev,
                                const void* w1, int64_t ldw1, const void* w2, int64_t ldw2, int64_t r,
-                               const void* teacher, int t_dtype, int64_t ldt, const int64_t* labels,
-                               const float* weights, const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k,
-                               float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats,
-                               float* metrics, void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+                               const void* teacher, int t_dtype, int64_t ldt, const ns_teacher_args* teacher_args,
+                               const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n,
+                               int64_t d, int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl,
+                               int64_t ldd, float* row_stats, float* metrics, void* workspace,
+                               size_t workspace_bytes, ns_stream_t stream) {
   const ns::MarkovFactors f{prev, w1, w2, ldw1, ldw2, r};
-  return lmhead_fwd_checked(hidden, ldh, weight, ldw, nullptr, 0, &f, teacher, t_dtype, ldt, labels, weights, valid,
-                            n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, workspace, workspace_bytes,
-                            stream, "ns_lmhead_markov_ce_kl_fwd");
+  return lmhead_fwd_checked(hidden, ldh, weight, ldw, nullptr, 0, &f, teacher, t_dtype, ldt, teacher_args, labels,
+                            weights, valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, workspace,
+                            workspace_bytes, stream, "ns_lmhead_markov_ce_kl_fwd");
+}
+
+int ns_lmhead_teacher_logits(const void* x, int64_t ldx, const int64_t* rows, int64_t n_rows, const void* weight,
+                             int64_t ldw, void* out, int64_t ldo, float* lse, int64_t n, int64_t v, int64_t d,
+                             void* workspace, size_t workspace_bytes, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
+  if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
+  if (d < 64 || d % 64) return fail(NS_EINVAL, "hidden size must be a positive multiple of 64 (got %lld)", (long long)d);
+  const int64_t nx = rows ? n_rows : n;
+  if (rows && (nx < 1 || nx >= (int64_t(1) << 31)))
+    return fail(NS_EINVAL, "n_rows must be in [1, 2^31) (got %lld)", (long long)nx);
+  int rc;
+  if ((rc = check_matrix(x, nx, d, ldx, "x"))) return rc;
+  if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
+  if ((rc = check_matrix(out, n, v, ldo, "out"))) return rc;
+  if (n > 0 && rows == nullptr && n_rows != 0 && n_rows != n)
+    return fail(NS_EINVAL, "n_rows %lld without rows must equal n", (long long)n_rows);
+  // gathered x rows are addressed with 32-bit byte offsets from its base
+  if (rows && nx * ldx * 2 >= (int64_t(1) << 32))
+    return fail(NS_EINVAL, "x spans %lld bytes; at most 4 GiB with rows", (long long)(nx * ldx * 2));
+  if (!aligned(x) || !aligned(weight) || !aligned(out) || ldx % 8 || ldw % 8 || ldo % 8)
+    return fail(NS_EALIGN, "teacher head needs 16-byte aligned base pointers and rows");
+  if (lse) {
+    const size_t need = ns::lmhead_linear_lse_workspace_bytes(n, v);
+    if (n > 0 && (!workspace || workspace_bytes < need))
+      return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  }
+  return hip_status(ns::lmhead_linear_lse(x, ldx, rows, nx, weight, ldw, nullptr, 0, out, ldo, lse, n, v, d, workspace,
+                                          reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_teacher_logits");
 }
 
 int ns_lmhead_bwd(const void* dl, int64_t ldd, const void* weight, int64_t ldw, void* dh, int64_t lddh,
@@ -374,7 +418,7 @@ int ns_lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw
 }
 
 int ns_fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const float* scale,
-                          void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, void* workspace,
+                          void* out, int64_t ldo, float* lse, int64_t n, int64_t v, int64_t d, void* workspace,
                           size_t workspace_bytes, ns_stream_t stream) {
   if (n < 0) return fail(NS_EINVAL, "n must be >= 0");
   if (v < 128 || v % 128 || d < 128 || d % 128) return fail(NS_EINVAL, "Expected checkpoint's 128x128 FP8 weight blocks");
@@ -385,11 +429,11 @@ int ns_fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t
   if (!scale) return fail(NS_ENULL, "scale is NULL");
   if (!aligned(x) || !aligned(wq) || !aligned(out) || ldx % 8 || ldw % 16 || ldo % 8)
     return fail(NS_EALIGN, "fp8 head needs 16-byte aligned base pointers and rows");
-  const size_t need = ns::fp8_workspace_bytes(n, d);
+  const size_t need = ns::fp8_workspace_bytes(n, v, d);
   if (n > 0 && (!workspace || workspace_bytes < need))
     return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
-  return hip_status(ns::fp8_teacher_logits(x, ldx, wq, ldw, scale, out, ldo, n, v, d, workspace,
+  return hip_status(ns::fp8_teacher_logits(x, ldx, wq, ldw, scale, out, ldo, lse, n, v, d, workspace,
                                            reinterpret_cast<hipStream_t>(stream)),
                     "ns_fp8_teacher_logits");
 }

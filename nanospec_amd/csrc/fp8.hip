@@ -68,6 +68,7 @@ struct Fp8Params {
   int64_t ldo;
   int64_t n, v, d;
   int tt, vt, splits, xa;  // token tiles, vocab tiles, vocab splits, XCD block (wg_coords)
+  RowPart* part;           // [N][splits] (max, sum-exp) of the stored bf16 values, or null
 };
 
 // Workgroup tile: 256 vocab rows (two weight-scale row blocks) x 128 tokens, 4 waves as
@@ -81,9 +82,11 @@ constexpr int kAStage = FM * kQBlock;        // 32 KB of weight codes
 constexpr int kBStage = FN * kQBlock;        // 16 KB of activation codes
 constexpr int kStage = kAStage + kBStage;
 constexpr int kRing = 3;
-constexpr int kFp8Lds = kRing * kStage;      // 144 KB
+constexpr int kRingLds = kRing * kStage;     // 144 KB
+constexpr int kLseOff = kRingLds;            // [FN][2] fp32 running (max, sum-exp) per token
+constexpr int kFp8Lds = kLseOff + FN * 8;
 constexpr int kOutRow = FM * 2 + 16;         // bf16 output row in the LDS transpose (+16 B)
-static_assert(FN * kOutRow <= kFp8Lds, "output transpose fits in the ring");
+static_assert(FN * kOutRow <= kRingLds, "output transpose fits in the ring");
 
 // s_waitcnt vmcnt(12) lgkmcnt(0) (expcnt not waited): gfx9 encoding, vmcnt[3:0] in bits
 // 3:0, expcnt in 6:4, lgkmcnt in 11:8, vmcnt[5:4] in 15:14.
@@ -106,6 +109,28 @@ __device__ __forceinline__ i32x8_t join(const u32x4_t& lo, const u32x4_t& hi) {
 __device__ __forceinline__ f32x16_t mfma_f8(const u32x4_t (&a)[2], const u32x4_t (&b)[2], const f32x16_t& c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(join(a[0], a[1]), join(b[0], b[1]), c, 0, 0, 0, 127, 0,
                                                           127);
+}
+
+// Reductions over the 16 lanes of a DPP row with every lane receiving the result:
+// xor 1, xor 2, then the half-row and row mirrors, which pair the 4- and 8-lane groups
+// once their values agree (so all 16 lanes end with the same bits).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_mov<0xB1>(x));
+  x = fmaxf(x, dpp_mov<0x4E>(x));
+  x = fmaxf(x, dpp_mov<0x141>(x));
+  return fmaxf(x, dpp_mov<0x140>(x));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_mov<0xB1>(x);
+  x += dpp_mov<0x4E>(x);
+  x += dpp_mov<0x141>(x);
+  return x + dpp_mov<0x140>(x);
 }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -134,6 +159,11 @@ void fp8_head_kernel(Fp8Params p) {
   for (int j = 0; j < 2; ++j) {
     const int64_t t = t0 + wn * 64 + j * 32 + r;
     xsrow[j] = p.xs + (t < p.n ? t : p.n - 1) * KB;
+  }
+  lds_f32* lse_st = reinterpret_cast<lds_f32*>(lds + kLseOff);
+  if (p.part && tid < FN) {   // first read after the first tile's barriers
+    lse_st[2 * tid] = kNegBig;
+    lse_st[2 * tid + 1] = 0.f;
   }
 
   for (int vt = vt_begin; vt < vt_end; ++vt) {
@@ -287,18 +317,81 @@ void fp8_head_kernel(Fp8Params p) {
           *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + tl * kOutRow + vl * 2) = y;
         }
     __syncthreads();
-#pragma unroll 4
-    for (int i = 0; i < FN * (FM / 8) / kThreads; ++i) {
+    // 16 lanes per output row (one DPP row), each taking 16-byte chunks c and c + 16
+#pragma unroll 2
+    for (int i = 0; i < FN * (FM / 16) / kThreads; ++i) {
       const int ci = i * kThreads + tid;
-      const int row = ci >> 5, c16 = ci & 31;
-      const int64_t t = t0 + row, v = v0 + c16 * 8;
-      if (t < p.n && v < p.v) {
-        const u32x4_t x = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + row * kOutRow + c16 * 16);
-        *reinterpret_cast<uint4*>(p.out + t * p.ldo + v) = make_uint4(x[0], x[1], x[2], x[3]);
+      const int row = ci >> 4, c = ci & 15;
+      const int64_t t = t0 + row;
+      float f[2][8];
+      bool in[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int chunk = c + 16 * h;
+        const int64_t v = v0 + chunk * 8;
+        in[h] = t < p.n && v < p.v;
+        const u32x4_t x =
+            *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + row * kOutRow + chunk * 16);
+        if (in[h]) *reinterpret_cast<uint4*>(p.out + t * p.ldo + v) = make_uint4(x[0], x[1], x[2], x[3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f[h][2 * e] = bf16_lo(x[e]);
+          f[h][2 * e + 1] = bf16_hi(x[e]);
+        }
+      }
+      if (p.part) {
+        // log-sum-exp of the stored bf16 row over this tile: the row maximum first, then
+        // one exponential per entry against it, then the sum
+        float m = kNegBig;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (in[h]) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, f[h][e]);
+          }
+        m = row16_max(m);
+        const float ml = m * kLog2e;
+        float sum = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (in[h]) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += fast_exp2(__builtin_fmaf(f[h][e], kLog2e, -ml));
+          }
+        sum = row16_sum(sum);
+        if (c == 0) {
+          const LseState r2 = lse_merge(LseState{lse_st[2 * row], lse_st[2 * row + 1]}, LseState{m, sum});
+          lse_st[2 * row] = r2.m;
+          lse_st[2 * row + 1] = r2.s;
+        }
       }
     }
     __syncthreads();
   }
+  if (p.part && tid < FN && t0 + tid < p.n) {
+    RowPart rp;
+    rp.mz = lse_st[2 * tid]; rp.sz = lse_st[2 * tid + 1];
+    rp.mu = kNegBig; rp.su = 0.f; rp.A = 0.f; rp.pad0 = rp.pad1 = rp.pad2 = 0.f;
+    p.part[(t0 + tid) * p.splits + split] = rp;
+  }
+}
+
+struct Fp8Plan {
+  int tt, vt, splits, xa;
+};
+
+Fp8Plan fp8_plan(int64_t n, int64_t v) {
+  Fp8Plan pl;
+  pl.vt = (int)((v + FM - 1) / FM);
+  pl.tt = (int)((n + FN - 1) / FN);
+  int cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  int sp = (cus + pl.tt - 1) / pl.tt;
+  sp = sp < 1 ? 1 : (sp > pl.vt ? pl.vt : sp);
+  pl.splits = sp;
+  pl.xa = xcd_block(pl.tt, sp);
+  return pl;
 }
 
 }  // namespace
@@ -313,15 +406,19 @@ hipError_t fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, u
   return hipGetLastError();
 }
 
-size_t fp8_workspace_bytes(int64_t n, int64_t d) {
-  return align_up((size_t)n * d, 256) + align_up((size_t)n * (d / kQBlock) * sizeof(float), 256);
+size_t fp8_workspace_bytes(int64_t n, int64_t v, int64_t d) {
+  const size_t part = v > 0 ? align_up((size_t)n * fp8_plan(n, v).splits * sizeof(RowPart), 256) : 0;
+  return align_up((size_t)n * d, 256) + align_up((size_t)n * (d / kQBlock) * sizeof(float), 256) + part;
 }
 
 hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const float* scale,
-                              void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st) {
+                              void* out, int64_t ldo, float* lse, int64_t n, int64_t v, int64_t d, void* ws,
+                              hipStream_t st) {
   if (n == 0 || v == 0) return hipSuccess;
   uint8_t* qx = static_cast<uint8_t*>(ws);
   float* xs = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)n * d, 256));
+  RowPart* part = reinterpret_cast<RowPart*>(static_cast<char*>(ws) + align_up((size_t)n * d, 256) +
+                                             align_up((size_t)n * (d / kQBlock) * sizeof(float), 256));
   {
     hipError_t e = fp8_quantize_rows(x, ldx, n, d, qx, xs, st);
     if (e != hipSuccess) return e;
@@ -330,15 +427,10 @@ hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int
   p.qx = qx; p.xs = xs; p.wq = wq; p.ws = scale; p.ldw = ldw;
   p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
   p.n = n; p.v = v; p.d = d;
-  p.vt = (int)((v + FM - 1) / FM);
-  p.tt = (int)((n + FN - 1) / FN);
-  int cus = 0, dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  int sp = (cus + p.tt - 1) / p.tt;
-  sp = sp < 1 ? 1 : (sp > p.vt ? p.vt : sp);
-  p.splits = sp;
-  p.xa = xcd_block(p.tt, sp);
+  const Fp8Plan pl = fp8_plan(n, v);
+  p.vt = pl.vt; p.tt = pl.tt; p.splits = pl.splits; p.xa = pl.xa;
+  const int sp = pl.splits;
+  p.part = lse ? part : nullptr;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_head_kernel),
@@ -346,9 +438,13 @@ hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  NS_TIMED("fp8_head_gemm", st);
-  hipLaunchKernelGGL(fp8_head_kernel, dim3((unsigned)(p.tt * sp)), dim3(kThreads), kFp8Lds, st, p);
-  return hipGetLastError();
+  {
+    NS_TIMED("fp8_head_gemm", st);
+    hipLaunchKernelGGL(fp8_head_kernel, dim3((unsigned)(p.tt * sp)), dim3(kThreads), kFp8Lds, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !lse) return e;
+  }
+  return launch_lse_merge(part, sp, n, lse, st);
 }
 
 }  // namespace ns

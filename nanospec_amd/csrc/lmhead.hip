@@ -547,9 +547,24 @@ struct HeadParams {
   int64_t ldd;
   uint16_t* out;            // MODE_STORE output [N, V] bf16
   int64_t ldo;
+  // teacher rows (the gather of train.py:285-290): objective row t reads teacher row
+  // trows[t] of nt rows; an index outside [0, nt) makes the row's teacher NaN.  null: row t
+  const int64_t* trows;
+  int64_t nt;
+  // teacher log-normalisers from the teacher's producer, one per teacher row (kTeacherLse):
+  // pass 1 reads no teacher, pass 2 writes partk[N][splits] = sum t (u - z) for KL
+  const float* tlse;
+  float* partk;
+  // MODE_STORE: B rows gathered as hidden[hrows[t]] of nh rows (null: row t); with
+  // kStoreLse, part1 receives the (max, sum-exp) partials of the stored bf16 values
+  const int64_t* hrows;
+  int64_t nh;
 };
 
 enum { MODE_STATS = 0, MODE_EMIT = 1, MODE_STORE = 2 };
+// head_kernel variants: the teacher's log-normaliser is given (STATS / EMIT), the stored
+// values' log-sum-exp partials are formed (STORE)
+enum { kTeacherLse = 1, kStoreLse = 2 };
 
 // Head-kernel LDS beyond the GEMM stages / epilogue dump: per-token running state and
 // per-token constants of the workgroup's 256 tokens (they persist across vocab tiles).
@@ -558,7 +573,10 @@ constexpr int kConstOff = kStateOff + 256 * 8 * 4;    // [256][8] fp32: lzl lul 
 constexpr int kLabelOff = kConstOff + 256 * 8 * 4;    // [256] int64 labels
 constexpr int kPrevOff = kLabelOff + 256 * 8;        // [256] int32 W1 rows (ids clamped to [0, V))
 constexpr int kBadOff = kPrevOff + 256 * 4;          // [256] uint8: id outside [0, V)
-constexpr int kHeadLdsBytes = kBadOff + 256;
+constexpr int kTrowOff = kBadOff + 256;             // [256] int32 teacher rows (0 when out of range)
+constexpr int kTbadOff = kTrowOff + 256 * 4;        // [256] uint8: teacher (STORE: B) row out of range
+constexpr int kHrowOff = kTbadOff + 256;            // [256] int32 gathered B rows (MODE_STORE)
+constexpr int kHeadLdsBytes = kHrowOff + 256 * 4;
 static_assert(kHeadLdsBytes <= 160 * 1024, "head kernel LDS");
 static_assert(kGemmLds <= kDumpLds, "the dump region covers the GEMM stages");
 
@@ -593,6 +611,26 @@ __device__ __forceinline__ float sum_reduce8(float x) {
   return x + dpp_partner<2>(x);
 }
 
+// One distribution's online (max, sum-exp): fold W values, and combine over 8 lanes.
+template <int W>
+__device__ __forceinline__ void lse_update(LseState& st, const float* z) {
+  float b = z[0];
+#pragma unroll
+  for (int i = 1; i < W; ++i) b = fmaxf(b, z[i]);
+  const float m = fmaxf(st.m, b);
+  const float ml = m * kLog2e;
+  float s = st.s * fast_exp2((st.m - m) * kLog2e);
+#pragma unroll
+  for (int i = 0; i < W; ++i) s += fast_exp2(__builtin_fmaf(z[i], kLog2e, -ml));
+  st = {m, s};
+}
+
+__device__ __forceinline__ LseState lse_reduce8(LseState a) {
+  a = lse_merge(a, LseState{dpp_partner<0>(a.m), dpp_partner<0>(a.s)});
+  a = lse_merge(a, LseState{dpp_partner<1>(a.m), dpp_partner<1>(a.s)});
+  return lse_merge(a, LseState{dpp_partner<2>(a.m), dpp_partner<2>(a.s)});
+}
+
 // Objective epilogue for one 128-token half of the tile, dumped in LDS as
 // zt[token][vocab] (kZRow floats per token).  Wave w owns tokens 32w .. 32w + 31 of the
 // half in four groups of eight; in a group, lane 8r + c takes token 8g + r and the
@@ -603,8 +641,10 @@ __device__ __forceinline__ float sum_reduce8(float x) {
 // running state in LDS.  Sums over a tile are formed locally first: one running fp32
 // sum over a whole vocab range (up to ~10^5 terms) would lose the many small terms.
 // V % 8 == 0, so each 8-entry chunk is wholly inside or outside the vocabulary.
-template <int MODE, typename TT>
+template <int MODE, typename TT, int FLAGS>
 __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, int half, int64_t t0, int64_t v0) {
+  // the teacher is read in pass 2, and in pass 1 unless its log-normaliser is given
+  constexpr bool kReadU = MODE == MODE_EMIT || (MODE == MODE_STATS && !(FLAGS & kTeacherLse));
   const lds_f32* zt = reinterpret_cast<const lds_f32*>(lds);
   lds_f32* state = reinterpret_cast<lds_f32*>(lds + kStateOff);
   const lds_f32* cst = reinterpret_cast<const lds_f32*>(lds + kConstOff);
@@ -622,7 +662,9 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
     const lds_f32* zr = zt + tl * kZRow;
     const bool has_m = p.markov != nullptr;   // kernel argument: uniform, so no divergent branch
     const uint16_t* mrow = (has_m ? p.markov : p.weight) + (has_m ? trow * p.ldm + v0 : 0);
-    const TT* urow = MODE == MODE_STORE ? nullptr : static_cast<const TT*>(p.teacher) + trow * p.ldt + v0;
+    const int trw = reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk];
+    const bool ubad = reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kTbadOff)[tk];
+    const TT* urow = kReadU ? static_cast<const TT*>(p.teacher) + (int64_t)trw * p.ldt + v0 : nullptr;
     float z[32], u[32];
     bool ok[4];
     // loads are unconditional (chunks past V re-read the row's first chunk) and the
@@ -635,7 +677,7 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
       const int vl = 8 * c8 + 64 * k;
       ok[k] = v0 + vl < p.v;
       vc[k] = ok[k] ? vl : 0;
-      if (MODE != MODE_STORE) uraw[k].load(urow + vc[k]);
+      if (kReadU) uraw[k].load(urow + vc[k]);
     }
     if (has_m) {
 #pragma unroll
@@ -660,24 +702,50 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
 #pragma unroll
         for (int e = 0; e < 8; ++e) mk[e] = __builtin_nanf("");
       }
-      if (MODE != MODE_STORE) uraw[k].unpack(u + 8 * k);
+      if (kReadU) uraw[k].unpack(u + 8 * k);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        z[8 * k + e] = ok[k] ? z[8 * k + e] + mk[e] : kNegBig;
-        if (MODE != MODE_STORE) u[8 * k + e] = ok[k] ? u[8 * k + e] : kNegBig;
+        // a gathered B row (MODE_STORE) outside its matrix: the output row is NaN
+        const float zk = MODE == MODE_STORE && ubad ? __builtin_nanf("") : z[8 * k + e] + mk[e];
+        z[8 * k + e] = ok[k] ? zk : kNegBig;
+        // a teacher row outside the teacher tensor: NaN (the reference's gather raises)
+        if (kReadU) u[8 * k + e] = ok[k] ? (ubad ? __builtin_nanf("") : u[8 * k + e]) : kNegBig;
       }
     }
     if (MODE == MODE_STORE) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         if (ok[k] && tok_ok) store8(p.out + t * p.ldo + v0 + 8 * c8 + 64 * k, z + 8 * k);
+      if (FLAGS & kStoreLse) {
+        // log-sum-exp of the values as stored (bf16), which is what a consumer reads
+#pragma unroll
+        for (int i = 0; i < 32; ++i) z[i] = bf16_to_f32(f32_to_bf16(z[i]));
+        LseState loc = {kNegBig, 0.f};
+        if (ok[0]) lse_update<32>(loc, z);
+        loc = lse_reduce8(loc);
+        if (c8 == 0) {
+          lds_f32* sr = state + tk * 8;
+          const LseState r = lse_merge(LseState{sr[0], sr[1]}, loc);
+          sr[0] = r.m; sr[1] = r.s;
+        }
+      }
       continue;
     }
     const int64_t y = lab[tk];
     const int64_t yr = y - v0;
     // this lane holds z_y (labels outside [0, V) match nothing; the merge flags them)
     const bool mine = yr >= 0 && yr < BM && y < p.v && ((yr >> 3) & 7) == c8 && tok_ok;
-    if (MODE == MODE_STATS) {
+    if (MODE == MODE_STATS && (FLAGS & kTeacherLse)) {
+      LseState loc = {kNegBig, 0.f};
+      if (ok[0]) lse_update<32>(loc, z);
+      loc = lse_reduce8(loc);
+      if (c8 == 0) {
+        lds_f32* sr = state + tk * 8;
+        const LseState r = lse_merge(LseState{sr[0], sr[1]}, loc);
+        sr[0] = r.m; sr[1] = r.s;
+      }
+      if (mine) p.zy[t] = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
+    } else if (MODE == MODE_STATS) {
       PairState loc = pair_init();
       // ok[] falls with k: a lane with no valid chunk keeps the empty state (an update
       // with every entry at the sentinel would form inf - inf)
@@ -692,7 +760,7 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
     } else {
       const lds_f32* cr = cst + tk * 8;
       const float lzl = cr[0], lul = cr[1], cp = cr[2], ct = cr[3], cy = cr[4];
-      float aloc = 0.f;
+      float aloc = 0.f, kloc = 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         float d[8];
@@ -701,16 +769,22 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
           const float pp = fast_exp2(__builtin_fmaf(z[8 * k + e], kLog2e, -lzl));
           const float tt = fast_exp2(__builtin_fmaf(u[8 * k + e], kLog2e, -lul));
           aloc += fminf(pp, tt);
+          // KL's sum t (u - z) (entries past V: t = 0 and u = z)
+          if (FLAGS & kTeacherLse) kloc = __builtin_fmaf(tt, u[8 * k + e] - z[8 * k + e], kloc);
           d[e] = __builtin_fmaf(cp, pp, -ct * tt);
         }
         if (p.dl && ok[k] && tok_ok) store8(p.dl + t * p.ldd + v0 + 8 * c8 + 64 * k, d);
       }
       aloc = sum_reduce8(aloc);
       if (c8 == 0) state[tk * 8] += aloc;
+      if (FLAGS & kTeacherLse) {
+        kloc = sum_reduce8(kloc);
+        if (c8 == 0) state[tk * 8 + 1] += kloc;
+      }
       // the label entry: rewrite dl[y] with the -c_ce term (same lane, after its store)
       if (mine && p.dl) {
         const float zy = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
-        const float uy = load1(urow + yr);
+        const float uy = ubad ? __builtin_nanf("") : load1(urow + yr);
         const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
         const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
         store1(p.dl + t * p.ldd + y, __builtin_fmaf(cp, pp, -ct * tt) - cy);
@@ -719,7 +793,7 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
   }
 }
 
-template <int MODE, typename TT>
+template <int MODE, typename TT, int FLAGS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void head_kernel(HeadParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
@@ -741,6 +815,26 @@ void head_kernel(HeadParams p) {
     reinterpret_cast<__attribute__((address_space(3))) int*>(lds + kPrevOff)[tid] = ok ? (int)id : 0;
     reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tid] = ok ? 0 : 1;
   }
+  {
+    // teacher row (MODE_STORE: gathered B row) of token tid, checked against its tensor
+    const int64_t t = t0 + tid;
+    const int64_t trow = t < p.n ? t : p.n - 1;
+    const int64_t* rows = MODE == MODE_STORE ? p.hrows : p.trows;
+    const int64_t lim = MODE == MODE_STORE ? p.nh : p.nt;
+    const int64_t rr = rows ? rows[trow] : trow;
+    const bool ok = !rows || (rr >= 0 && rr < lim);
+    reinterpret_cast<__attribute__((address_space(3))) int*>(lds + kTrowOff)[tid] = ok ? (int)rr : 0;
+    reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds + kTbadOff)[tid] = ok ? 0 : 1;
+    if (MODE == MODE_STORE)
+      reinterpret_cast<__attribute__((address_space(3))) int*>(lds + kHrowOff)[tid] = ok ? (int)rr : 0;
+  }
+  if (MODE == MODE_STORE && (FLAGS & kStoreLse)) {
+    lds_f32* sr = reinterpret_cast<lds_f32*>(lds + kStateOff) + tid * 8;
+    sr[0] = kNegBig;
+    sr[1] = 0.f;
+  }
+  // gathered B rows are read from LDS by every wave's fill offsets before the first barrier
+  if (MODE == MODE_STORE && p.hrows) __syncthreads();
   if (MODE != MODE_STORE) {
     const int64_t t = t0 + tid;
     const int64_t trow = t < p.n ? t : p.n - 1;
@@ -764,7 +858,16 @@ void head_kernel(HeadParams p) {
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int64_t v0 = (int64_t)vt * BM;
     zero_acc(acc);
-    gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds);
+    if (MODE == MODE_STORE && p.hrows) {   // B = hidden[hrows[t-tile]]
+      const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+      DmaTile<256> ta, tb;
+      ta.init(p.ldw * 2, v0, p.v, wv);
+      tb.init_gather(p.ldh * 2, reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kHrowOff), wv);
+      gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.weight + v0 * p.ldw), tb,
+                    reinterpret_cast<const char*>(p.hidden), (int)(p.d / BK), lds);
+    } else {
+      gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds);
+    }
     if (p.r > 0) {   // Markov K segment: W2[v-tile] . W1[prev[t-tile]]^T
       const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
       DmaTile<256> ta, tb;
@@ -777,23 +880,29 @@ void head_kernel(HeadParams p) {
     for (int jj = 0; jj < 2; ++jj) {
       if (wn == jj) dump_half(acc, lds);
       __syncthreads();
-      epilogue_half<MODE, TT>(p, lds, jj, t0, v0);
+      epilogue_half<MODE, TT, FLAGS>(p, lds, jj, t0, v0);
       __syncthreads();
     }
   }
 
-  if (MODE == MODE_STORE) return;
+  if (MODE == MODE_STORE && !(FLAGS & kStoreLse)) return;
   // this split's partial of every token (state complete: the last epilogue ended with a barrier)
   const int64_t t = t0 + tid;
   if (t < p.n) {
     const lds_f32* sr = reinterpret_cast<const lds_f32*>(lds + kStateOff) + tid * 8;
-    if (MODE == MODE_STATS) {
+    if (MODE == MODE_STATS || MODE == MODE_STORE) {
+      // teacher-free pass 1 and the stored values' partials carry (mz, sz) only
+      const bool pair = MODE == MODE_STATS && !(FLAGS & kTeacherLse);
       RowPart rp;
-      rp.mz = sr[0]; rp.sz = sr[1]; rp.mu = sr[2]; rp.su = sr[3]; rp.A = sr[4];
+      rp.mz = sr[0]; rp.sz = sr[1];
+      rp.mu = pair ? sr[2] : kNegBig;
+      rp.su = pair ? sr[3] : 0.f;
+      rp.A = pair ? sr[4] : 0.f;
       rp.pad0 = rp.pad1 = rp.pad2 = 0.f;
       p.part1[t * p.splits + split] = rp;
     } else {
       p.parta[t * p.splits + split] = sr[0];
+      if (FLAGS & kTeacherLse) p.partk[t * p.splits + split] = sr[1];
     }
   }
 }
@@ -955,6 +1064,7 @@ struct HeadWs {
   RowPart* part1;
   float* parta;
   float* zy;
+  float* partk;   // pass-2 KL partials (teacher log-normaliser given)
 };
 
 size_t head_ws_layout(int64_t n, int64_t v, void* base, HeadWs* out) {
@@ -967,8 +1077,9 @@ size_t head_ws_layout(int64_t n, int64_t v, void* base, HeadWs* out) {
     out->part1 = reinterpret_cast<RowPart*>(c);
     out->parta = reinterpret_cast<float*>(c + b1);
     out->zy = reinterpret_cast<float*>(c + b1 + b2);
+    out->partk = reinterpret_cast<float*>(c + b1 + b2 + b3);
   }
-  return b1 + b2 + b3;
+  return b1 + b2 + b3 + b2;
 }
 
 struct BwdPlan {
@@ -1018,29 +1129,31 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   return pl;
 }
 
-template <int MODE, typename TT>
+template <int MODE, typename TT, int FLAGS = 0>
 hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char* name) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<MODE, TT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kHeadLdsBytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   NS_TIMED(name, st);
-  hipLaunchKernelGGL((head_kernel<MODE, TT>), dim3(grid), dim3(kThreads), kHeadLdsBytes, st, p);
+  hipLaunchKernelGGL((head_kernel<MODE, TT, FLAGS>), dim3(grid), dim3(kThreads), kHeadLdsBytes, st, p);
   return hipGetLastError();
 }
 
-template <typename TT>
+template <typename TT, int FLAGS>
 hipError_t head_forward_typed(HeadParams& p, const HeadPlan& pl, const SlotArgs& a, float* row_stats,
                               float* metrics, const HeadWs& w, hipStream_t st) {
-  hipError_t e = launch_head<MODE_STATS, TT>(p, pl.grid, st, "head_stats");
+  hipError_t e = launch_head<MODE_STATS, TT, FLAGS>(p, pl.grid, st, "head_stats");
   if (e != hipSuccess) return e;
-  if ((e = launch_merge(w.part1, w.zy, p.v, pl.splits, a, row_stats, st)) != hipSuccess) return e;
+  const TeacherSpec tl{p.trows, p.nt, p.tlse};
+  if ((e = launch_merge(w.part1, w.zy, p.v, pl.splits, a, row_stats, st, p.tlse ? &tl : nullptr)) != hipSuccess)
+    return e;
   p.row_stats = row_stats;
-  if ((e = launch_head<MODE_EMIT, TT>(p, pl.grid, st, "head_emit")) != hipSuccess) return e;
-  return launch_finalize(w.parta, pl.splits, a, row_stats, metrics, st);
+  if ((e = launch_head<MODE_EMIT, TT, FLAGS>(p, pl.grid, st, "head_emit")) != hipSuccess) return e;
+  return launch_finalize(w.parta, pl.splits, a, row_stats, metrics, st, p.tlse ? w.partk : nullptr);
 }
 
 }  // namespace
@@ -1052,8 +1165,8 @@ size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d) {
 
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
                           int64_t ldm, const MarkovFactors* factors, const void* teacher, int tdt, int64_t ldt,
-                          int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd, float* row_stats,
-                          float* metrics, void* ws, hipStream_t st) {
+                          int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts, void* dl, int64_t ldd,
+                          float* row_stats, float* metrics, void* ws, hipStream_t st) {
   if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
   const HeadPlan pl = head_plan(a.n, v);
   HeadWs w;
@@ -1068,16 +1181,23 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
   p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa;
   p.labels = a.labels; p.weights = a.weights;
   p.c_ce = a.c_ce; p.c_kl = a.c_kl; p.inv_acc = a.inv_acc;
-  p.part1 = w.part1; p.zy = w.zy; p.parta = w.parta;
+  p.part1 = w.part1; p.zy = w.zy; p.parta = w.parta; p.partk = w.partk;
   p.dl = static_cast<uint16_t*>(dl); p.ldd = ldd;
+  if (ts) {
+    p.trows = ts->rows; p.nt = ts->nt; p.tlse = ts->lse;
+  }
   if (factors) {
     p.prev = factors->prev;
     p.w1 = static_cast<const uint16_t*>(factors->w1);
     p.w2 = static_cast<const uint16_t*>(factors->w2);
     p.ldw1 = factors->ldw1; p.ldw2 = factors->ldw2; p.r = factors->r;
   }
-  if (tdt == kBF16) return head_forward_typed<uint16_t>(p, pl, a, row_stats, metrics, w, st);
-  return head_forward_typed<float>(p, pl, a, row_stats, metrics, w, st);
+  if (p.tlse) {
+    if (tdt == kBF16) return head_forward_typed<uint16_t, kTeacherLse>(p, pl, a, row_stats, metrics, w, st);
+    return head_forward_typed<float, kTeacherLse>(p, pl, a, row_stats, metrics, w, st);
+  }
+  if (tdt == kBF16) return head_forward_typed<uint16_t, 0>(p, pl, a, row_stats, metrics, w, st);
+  return head_forward_typed<float, 0>(p, pl, a, row_stats, metrics, w, st);
 }
 
 size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r, bool norm) {
@@ -1145,6 +1265,17 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
 
 hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                          int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d, hipStream_t st) {
+  return lmhead_linear_lse(x, ldx, nullptr, 0, weight, ldw, addend, lda, out, ldo, nullptr, n, v, d, nullptr, st);
+}
+
+size_t lmhead_linear_lse_workspace_bytes(int64_t n, int64_t v) {
+  const HeadPlan pl = head_plan(n, v);
+  return align_up((size_t)n * pl.splits * sizeof(RowPart), 256);
+}
+
+hipError_t lmhead_linear_lse(const void* x, int64_t ldx, const int64_t* rows, int64_t nrows, const void* weight,
+                             int64_t ldw, const void* addend, int64_t lda, void* out, int64_t ldo, float* lse,
+                             int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st) {
   if (n == 0 || v == 0) return hipSuccess;
   const HeadPlan pl = head_plan(n, v);
   HeadParams p = {};
@@ -1156,7 +1287,12 @@ hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t
   p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa;
   p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
   p.teacher = nullptr;
-  return launch_head<MODE_STORE, uint16_t>(p, pl.grid, st, "head_linear");
+  p.hrows = rows; p.nh = nrows;
+  if (!lse) return launch_head<MODE_STORE, uint16_t, 0>(p, pl.grid, st, "head_linear");
+  p.part1 = static_cast<RowPart*>(ws);
+  hipError_t e = launch_head<MODE_STORE, uint16_t, kStoreLse>(p, pl.grid, st, "head_linear_lse");
+  if (e != hipSuccess) return e;
+  return launch_lse_merge(p.part1, pl.splits, n, lse, st);
 }
 
 }  // namespace ns

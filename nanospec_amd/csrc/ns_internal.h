@@ -31,12 +31,24 @@ hipError_t stream_backward(const void* z, int zdt, int64_t ldz, const void* u, i
                            hipStream_t st);
 
 // ---- shared tails (stream.hip) ---------------------------------------------
+// Teacher logits as the producer left them: objective row t reads teacher row rows[t]
+// (rows null: row t) of nt rows; lse (null: formed in pass 1) holds one log-normaliser per
+// teacher row.
+struct TeacherSpec {
+  const int64_t* rows;
+  int64_t nt;
+  const float* lse;
+};
 // Merge first-pass partials part1[N][S] (+ z_y[N]) into row_stats (lse_z, lse_u, ce, kl, z_y).
+// With ts (its lse given) lse_u comes from ts and KL is left to the finalize.
 hipError_t launch_merge(const RowPart* part1, const float* zy, int64_t v, int splits, const SlotArgs& a,
-                        float* row_stats, hipStream_t st);
-// Sum accept partials parta[N][S], form block lengths and the six metrics.
+                        float* row_stats, hipStream_t st, const TeacherSpec* ts = nullptr);
+// Sum accept partials parta[N][S], form block lengths and the six metrics; with partk
+// (pass-2 sums of t (u - z)), KL = sum partk - lse_u + lse_z first.
 hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, float* row_stats,
-                           float* metrics, hipStream_t st);
+                           float* metrics, hipStream_t st, const float* partk = nullptr);
+// lse[t] = log-sum-exp from (max, sum-exp) partials part1[N][S] (mz, sz), fixed order.
+hipError_t launch_lse_merge(const RowPart* part1, int splits, int64_t n, float* lse, hipStream_t st);
 
 // ---- final_norm around the head (norm.hip) ------------------------------------
 constexpr int64_t kMaxNormD = 16384;   // hidden sizes the rms-norm kernels hold in registers
@@ -71,8 +83,8 @@ struct MarkovFactors {
 size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d);
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
                           const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
-                          int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, void* dl, int64_t ldd,
-                          float* row_stats, float* metrics, void* ws, hipStream_t st);
+                          int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts,
+                          void* dl, int64_t ldd, float* row_stats, float* metrics, void* ws, hipStream_t st);
 // dh workspace; r > 0 adds the Markov column tiles' partials, norm the rms-norm
 // backward's column partials
 size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r = 0, bool norm = false);
@@ -94,13 +106,21 @@ hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int6
 hipError_t lmhead_linear(const void* x, int64_t ldx, const void* weight, int64_t ldw, const void* addend,
                          int64_t lda, void* out, int64_t ldo, int64_t n, int64_t v, int64_t d,
                          hipStream_t st);
+// The projection as a teacher-logit producer: out = x[rows] . weight^T (+ addend) with,
+// when lse is not NULL, lse[t] = log-sum-exp of out's bf16 row t; rows (null: row t)
+// index nrows rows of x.  Workspace: lmhead_linear_lse_workspace_bytes.
+size_t lmhead_linear_lse_workspace_bytes(int64_t n, int64_t v);
+hipError_t lmhead_linear_lse(const void* x, int64_t ldx, const int64_t* rows, int64_t nrows, const void* weight,
+                             int64_t ldw, const void* addend, int64_t lda, void* out, int64_t ldo, float* lse,
+                             int64_t n, int64_t v, int64_t d, void* ws, hipStream_t st);
 
 // ---- FP8 teacher head (fp8.hip) ---------------------------------------------
-size_t fp8_workspace_bytes(int64_t n, int64_t d);
+size_t fp8_workspace_bytes(int64_t n, int64_t v, int64_t d);
 hipError_t fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs,
                              hipStream_t st);
+// lse (null: not formed): log-sum-exp of each stored bf16 output row, from the epilogue
 hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw,
-                              const float* scale, void* out, int64_t ldo, int64_t n, int64_t v,
+                              const float* scale, void* out, int64_t ldo, float* lse, int64_t n, int64_t v,
                               int64_t d, void* ws, hipStream_t st);
 
 // ---- slot preparation (prepare.hip) -----------------------------------------

@@ -159,14 +159,19 @@ __global__ __launch_bounds__(kStreamThreads) void stream_stats_kernel(
 __global__ __launch_bounds__(256) void merge_kernel(const RowPart* __restrict__ part1,
                                                     const float* __restrict__ zy,
                                                     const int64_t* __restrict__ labels, int64_t v,
-                                                    int splits, int64_t n, float* __restrict__ row_stats) {
+                                                    int splits, int64_t n, float* __restrict__ row_stats,
+                                                    TeacherSpec ts) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= n) return;
   const RowPart* p = part1 + r * splits;
   PairState st = {p[0].mz, p[0].sz, p[0].mu, p[0].su, p[0].A};
   for (int s = 1; s < splits; ++s) st = pair_merge(st, PairState{p[s].mz, p[s].sz, p[s].mu, p[s].su, p[s].A});
   const float lz = st.mz + logf(st.sz);
-  const float lu = st.mu + logf(st.su);
+  float lu = st.mu + logf(st.su);
+  if (ts.lse) {   // the teacher's producer formed its log-normaliser; KL follows pass 2
+    const int64_t tr = ts.rows ? ts.rows[r] : r;
+    lu = (tr >= 0 && tr < ts.nt) ? ts.lse[tr] : __builtin_nanf("");
+  }
   // A label outside [0, V) has no logit: CE becomes NaN (the loss reports it, never masks it).
   const int64_t label = labels[r];
   const float y = (label >= 0 && label < v) ? zy[r] : __builtin_nanf("");
@@ -174,17 +179,38 @@ __global__ __launch_bounds__(256) void merge_kernel(const RowPart* __restrict__ 
   o[kLseZ] = lz;
   o[kLseU] = lu;
   o[kCE] = lz - y;
-  o[kKL] = st.A / st.su - lu + lz;
+  o[kKL] = ts.lse ? 0.f : st.A / st.su - lu + lz;
   o[kZy] = y;
+  o[6] = 0.f;   // reserved columns of the row_stats layout
+  o[7] = 0.f;
 }
 
 hipError_t launch_merge(const RowPart* part1, const float* zy, int64_t v, int splits, const SlotArgs& a,
-                        float* row_stats, hipStream_t st) {
+                        float* row_stats, hipStream_t st, const TeacherSpec* ts) {
   const int64_t blocks = (a.n + 255) / 256;
+  const TeacherSpec none{nullptr, 0, nullptr};
   NS_TIMED("merge_rows", st);
   if (blocks > 0)
     hipLaunchKernelGGL(merge_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part1, zy, a.labels, v,
-                       splits, a.n, row_stats);
+                       splits, a.n, row_stats, ts ? *ts : none);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void lse_merge_kernel(const RowPart* __restrict__ part1, int splits, int64_t n,
+                                                        float* __restrict__ lse) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const RowPart* p = part1 + r * splits;
+  LseState st = {p[0].mz, p[0].sz};
+  for (int s = 1; s < splits; ++s) st = lse_merge(st, LseState{p[s].mz, p[s].sz});
+  lse[r] = st.m + logf(st.s);
+}
+
+hipError_t launch_lse_merge(const RowPart* part1, int splits, int64_t n, float* lse, hipStream_t st) {
+  const int64_t blocks = (n + 255) / 256;
+  NS_TIMED("lse_merge", st);
+  if (blocks > 0)
+    hipLaunchKernelGGL(lse_merge_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part1, splits, n, lse);
   return hipGetLastError();
 }
 
@@ -306,14 +332,22 @@ constexpr int kFinalThreads = 1024;
 __global__ __launch_bounds__(kFinalThreads) void finalize_kernel(
     const float* __restrict__ parta, int splits, int64_t n, int64_t k, const float* __restrict__ weights,
     const uint8_t* __restrict__ valid, float c_ce, float c_kl, float* __restrict__ row_stats,
-    float* __restrict__ metrics) {
-  // phase 1: accept rate per row (fixed split order)
+    float* __restrict__ metrics, const float* __restrict__ partk) {
+  // phase 1: accept rate per row (fixed split order) and, with partk, KL per row
+  // (KL = sum t (u - z) - lse_u + lse_z, sum t = 1)
   if (parta != nullptr) {
     for (int64_t r = threadIdx.x; r < n; r += kFinalThreads) {
       const float* p = parta + r * splits;
       float a = p[0];
       for (int s = 1; s < splits; ++s) a += p[s];
-      row_stats[r * kRowStatWidth + kAccept] = a;
+      float* rs = row_stats + r * kRowStatWidth;
+      rs[kAccept] = a;
+      if (partk != nullptr) {
+        const float* q = partk + r * splits;
+        float k = q[0];
+        for (int s = 1; s < splits; ++s) k += q[s];
+        rs[kKL] = k - rs[kLseU] + rs[kLseZ];
+      }
     }
   }
   __syncthreads();
@@ -366,10 +400,10 @@ __global__ __launch_bounds__(kFinalThreads) void finalize_kernel(
 }
 
 hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, float* row_stats,
-                           float* metrics, hipStream_t st) {
+                           float* metrics, hipStream_t st, const float* partk) {
   NS_TIMED("finalize_metrics", st);
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kFinalThreads), 0, st, parta, splits, a.n, a.k,
-                     a.weights, a.valid, a.c_ce, a.c_kl, row_stats, metrics);
+                     a.weights, a.valid, a.c_ce, a.c_kl, row_stats, metrics, partk);
   return hipGetLastError();
 }
 

@@ -40,6 +40,56 @@ class MarkovFactors:
 
 
 @dataclass
+class TeacherLogits:
+    """Teacher logits as their producer left them (train.py:280-290).
+
+    logits [R, V] bf16 or fp32 (R teacher rows, e.g. the verifier's B*S positions);
+    rows [N] int64: the teacher row of each objective row -- the gather by
+    prepared.teacher_indices (``teacher_rows``), done inside the loads, with no gathered
+    copy; None: row t (R == N).  lse [R] fp32: the log-sum-exp of every teacher row when
+    its producer formed it (``teacher_logits``): the first pass then reads no teacher."""
+
+    logits: torch.Tensor
+    rows: torch.Tensor | None = None
+    lse: torch.Tensor | None = None
+
+
+def teacher_rows(teacher_indices, sequence_length):
+    """Flat teacher row of every objective row: b * S + teacher_indices[b, j], the rows
+    ``logits.gather(1, teacher_indices)`` selects from [B, S, V] (train.py:285-290)."""
+    ti = teacher_indices.to(torch.int64)
+    b = ti.shape[0]
+    base = torch.arange(b, device=ti.device, dtype=torch.int64).unsqueeze(-1) * int(sequence_length)
+    return (ti.reshape(b, -1) + base).reshape(-1).contiguous()
+
+
+@torch.no_grad()
+def teacher_logits(x, lm_head_weight, rows=None):
+    """Teacher logits from hidden states through the LM head (train.py:172-173, and
+    281-284 with the teacher's last hidden state gathered at teacher_indices): bf16
+    x[rows] . W^T, plus their log-sum-exp per row from the GEMM epilogue.  x [R, d] bf16
+    (any leading shape), rows [N] int64 or None.  Returns TeacherLogits(logits [N, V],
+    None, lse [N])."""
+    vocab, d = lm_head_weight.shape
+    device = _lib.require_device(x, lm_head_weight, rows)
+    a, lda = _bf16_rows(x, d, "x")
+    w, ldw = _bf16_rows(lm_head_weight, d, "lm_head_weight")
+    if rows is not None:
+        r = rows.reshape(-1).to(device=device, dtype=torch.int64).contiguous()
+        n, n_rows = r.numel(), a.shape[0]
+    else:
+        r, n, n_rows = None, a.shape[0], 0
+    out = torch.empty((n, vocab), dtype=torch.bfloat16, device=device)
+    lse = torch.empty(n, dtype=torch.float32, device=device)
+    ws = _lib.workspace(_lib.NS_WS_TEACHER_LOGITS, n, vocab, d, device)
+    status = _lib.load().ns_lmhead_teacher_logits(
+        _lib.ptr(a), lda, _lib.ptr(r), n_rows, _lib.ptr(w), ldw, _lib.ptr(out), vocab, _lib.ptr(lse), n, vocab, d,
+        _lib.ptr(ws), ws.numel(), _lib.stream(device))
+    _lib.check(status, "ns_lmhead_teacher_logits")
+    return TeacherLogits(out, None, lse)
+
+
+@dataclass
 class HeadActivations:
     """State the fused backward needs: per-row statistics, the emitted dl and the
     frozen head weight.  row_stats [N, 8] = (lse_z, lse_u, ce, kl, accept_rate, z_label, 0, 0)."""
@@ -65,7 +115,8 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
     """Fused forward: LM-head projection (+ Markov addend) and the CE + KL + accept objective.
 
     hidden [..., K, d] bf16; lm_head_weight [V, d] bf16; target_logits [..., K, V]
-    bf16 or fp32; markov_logits [..., K, V] bf16 or None; prepared has weights,
+    bf16 or fp32, or a ``TeacherLogits`` (teacher rows gathered in the loads, and the
+    producer's log-normalisers); markov_logits [..., K, V] bf16 or None; prepared has weights,
     target_ids, valid [..., K].  dl is emitted for ``accumulation_steps`` (pass the
     same value to the backward).  ``markov`` (a ``MarkovFactors``) adds the Markov
     head in factored form instead of a dense ``markov_logits`` tensor: it is fused
@@ -75,13 +126,26 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
     if accumulation_steps < 1:
         raise ValueError("accumulation_steps must be >= 1")
     vocab, d = lm_head_weight.shape
-    device = _lib.require_device(hidden, lm_head_weight, target_logits, markov_logits)
+    spec = target_logits if isinstance(target_logits, TeacherLogits) else TeacherLogits(target_logits)
+    device = _lib.require_device(hidden, lm_head_weight, spec.logits, spec.rows, spec.lse, markov_logits)
     lib = _lib.load()
     h, ldh = _bf16_rows(hidden, d, "hidden")
     w, ldw = _bf16_rows(lm_head_weight, d, "lm_head_weight")
     n = h.shape[0]
-    u, ldu = _lib.rows_2d(target_logits, vocab)
-    if u.shape[0] != n:
+    u, ldu = _lib.rows_2d(spec.logits, vocab)
+    keep = []
+    targs = None
+    if spec.rows is not None or spec.lse is not None:
+        rows = spec.rows.reshape(-1).to(device=device, dtype=torch.int64).contiguous() if spec.rows is not None \
+            else None
+        if rows is not None and rows.numel() != n:
+            raise ValueError(f"teacher rows has {rows.numel()} entries, hidden has {n} rows")
+        lse = spec.lse.reshape(-1).to(torch.float32).contiguous() if spec.lse is not None else None
+        if lse is not None and lse.numel() != u.shape[0]:
+            raise ValueError(f"teacher lse has {lse.numel()} entries, the teacher logits {u.shape[0]} rows")
+        keep = [rows, lse]
+        targs = _lib.TeacherArgs(_lib.ptr(rows), u.shape[0] if rows is not None else 0, _lib.ptr(lse))
+    if spec.rows is None and u.shape[0] != n:
         raise ValueError(f"target_logits has {u.shape[0]} rows, hidden has {n}")
     if markov_logits is not None:
         m, ldm = _bf16_rows(markov_logits, vocab, "markov_logits")
@@ -96,7 +160,7 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
     row_stats = torch.empty((n, 8), dtype=torch.float32, device=device)
     dl = torch.empty((n, vocab), dtype=torch.bfloat16, device=device) if emit_dlogits else None
     ws = _lib.workspace(_lib.NS_WS_LMHEAD, n, vocab, d, device)
-    tail = (_lib.ptr(u), _lib.dtype_code(u), ldu, _lib.ptr(y), _lib.ptr(wts), _lib.ptr(valid), n, d, vocab, k,
+    tail = (_lib.ptr(u), _lib.dtype_code(u), ldu, ctypes.byref(targs) if targs is not None else None, _lib.ptr(y), _lib.ptr(wts), _lib.ptr(valid), n, d, vocab, k,
             float(o.ce), float(o.kl), 1.0 / accumulation_steps, _lib.ptr(dl), vocab, _lib.ptr(row_stats),
             _lib.ptr(metrics), _lib.ptr(ws), ws.numel(), _lib.stream(device))
     if markov is None:
@@ -107,6 +171,7 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
         status = lib.ns_lmhead_markov_ce_kl_fwd(_lib.ptr(h), ldh, _lib.ptr(w), ldw, _lib.ptr(prev), _lib.ptr(w1),
                                                 ldw1, _lib.ptr(w2), ldw2, r, *tail)
         _lib.check(status, "ns_lmhead_markov_ce_kl_fwd")
+    del keep
     shape = tuple(hidden.shape[:-1]) + (vocab,)
     saved = HeadActivations(o, lm_head_weight, row_stats, dl, accumulation_steps, shape, markov)
     return LossMetrics.from_buffer(metrics), saved

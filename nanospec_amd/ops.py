@@ -41,6 +41,23 @@ def fp8_linear(x, weight, scale):
     """Reference quantisation, expanded scales, fp32 accumulation, bf16 output."""
     if weight.dtype != torch.float8_e4m3fn:
         return linear(x, weight)
+    return _fp8_linear(x, weight, scale, with_lse=False)[0]
+
+
+@torch.no_grad()
+def fp8_teacher_logits(x, weight, scale):
+    """Teacher logits from a block-FP8 head (ops.fp8_linear numerics) together with the
+    log-sum-exp of each bf16 output row, formed in the GEMM epilogue: a
+    ``head.TeacherLogits`` whose first pass reads no teacher logits."""
+    from nanospec_amd.head import TeacherLogits
+
+    if weight.dtype != torch.float8_e4m3fn:
+        raise ValueError(f"fp8_teacher_logits needs float8_e4m3fn weights (got {weight.dtype})")
+    out, lse = _fp8_linear(x, weight, scale, with_lse=True)
+    return TeacherLogits(out.reshape(-1, out.shape[-1]), None, lse)
+
+
+def _fp8_linear(x, weight, scale, with_lse):
     v, d = weight.shape
     if v % 128 or d % 128:
         raise ValueError("Expected checkpoint's 128x128 FP8 weight blocks")
@@ -55,13 +72,14 @@ def fp8_linear(x, weight, scale):
         raise ValueError(f"scale must be [{v // 128}, {d // 128}] (got {tuple(sc.shape)})")
     n = xr.shape[0]
     out = torch.empty((n, v), dtype=torch.bfloat16, device=device)
+    lse = torch.empty(n, dtype=torch.float32, device=device) if with_lse else None
     ws = _lib.workspace(_lib.NS_WS_FP8, n, v, d, device)
     status = _lib.load().ns_fp8_teacher_logits(
-        _lib.ptr(xr), ldx, _lib.ptr(wr), ldw, _lib.ptr(sc), _lib.ptr(out), v, n, v, d,
+        _lib.ptr(xr), ldx, _lib.ptr(wr), ldw, _lib.ptr(sc), _lib.ptr(out), v, _lib.ptr(lse), n, v, d,
         _lib.ptr(ws), ws.numel(), _lib.stream(device),
     )
     _lib.check(status, "ns_fp8_teacher_logits")
-    return out.view(tuple(x.shape[:-1]) + (v,))
+    return out.view(tuple(x.shape[:-1]) + (v,)), lse
 
 
 @torch.no_grad()

@@ -91,3 +91,47 @@ def test_c4_teacher_fused_with_draft_path(gpu_lib):
     np.testing.assert_allclose(rs[:, 2], r["ce"], rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(rs[:, 3], r["kl"], rtol=1e-4, atol=1e-4)
     assert np.isfinite(float(m.loss)) and 1.0 <= float(m.accept_len) <= 9.0
+
+
+def _lse64(x):
+    x = np.asarray(x, dtype=np.float64)
+    mx = x.max(-1, keepdims=True)
+    return (mx + np.log(np.exp(x - mx).sum(-1, keepdims=True)))[..., 0]
+
+
+@pytest.mark.parametrize("n,d,v", [(200, 384, 2048), (640, 256, 8192)])
+def test_fp8_teacher_lse_from_the_epilogue(gpu_lib, n, d, v):
+    """The producer's log-sum-exp of each bf16 output row (train.py:280-290's teacher,
+    C4's head): the same logits as fp8_linear, and their LSE in fp64 to 2e-6."""
+    g = torch.Generator(device=DEV).manual_seed(n)
+    x = torch.randn((n, d), generator=g, device=DEV).bfloat16()
+    w = 0.02 * torch.randn((v, d), generator=g, device=DEV)
+    blocks = w.view(v // 128, 128, d // 128, 128)
+    scale = blocks.abs().amax(dim=(1, 3)) / 448.0
+    codes = (blocks / scale[:, None, :, None]).clamp(-448, 448).reshape(v, d).to(torch.float8_e4m3fn)
+    plain = ops.fp8_linear(x, codes, scale)
+    spec = ops.fp8_teacher_logits(x, codes, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(spec.logits, plain)
+    np.testing.assert_allclose(_np(spec.lse), _lse64(_np(plain)), rtol=2e-6, atol=2e-6)
+
+
+def test_c4_teacher_once_with_fp8_lse(gpu_lib):
+    """C4 with the fp8 head's log-sum-exp: pass 1 reads no teacher; metrics agree with
+    the two-read forward to 2e-5 and the per-row CE / KL with the oracle to 1e-4."""
+    hidden, weight, markov, (xt, codes, scale), slots = synthetic.c4(DEV)
+    spec = ops.fp8_teacher_logits(xt, codes.view(torch.float8_e4m3fn), scale)
+    o = Objective(block_size=8)
+    m1, s1 = head.lm_head_ce_kl_loss(hidden, weight, spec, slots, o, markov_logits=markov)
+    m2, s2 = head.lm_head_ce_kl_loss(hidden, weight, spec.logits, slots, o, markov_logits=markov)
+    torch.cuda.synchronize()
+    for f in ("ce", "kl", "numerator", "denominator", "accept_len_sum", "accept_len_total"):
+        a, b = float(getattr(m1, f)), float(getattr(m2, f))
+        assert a == pytest.approx(b, rel=2e-5, abs=1e-6), f
+    rows = np.arange(8 * 300, 8 * 301)
+    z = ref.lm_head_logits(_np(hidden[rows]), _np(weight), _np(markov[rows]), dtype=np.float32)
+    y = slots.target_ids.reshape(-1)[rows].cpu().numpy()
+    r = ref.row_objective(z, _np(spec.logits[rows]), y)
+    rs = _np(s1.row_stats)[rows]
+    np.testing.assert_allclose(rs[:, 2], r["ce"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(rs[:, 3], r["kl"], rtol=1e-4, atol=1e-4)
