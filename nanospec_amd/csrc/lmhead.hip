@@ -641,7 +641,12 @@ __device__ __forceinline__ LseState lse_reduce8(LseState a) {
 // running state in LDS.  Sums over a tile are formed locally first: one running fp32
 // sum over a whole vocab range (up to ~10^5 terms) would lose the many small terms.
 // V % 8 == 0, so each 8-entry chunk is wholly inside or outside the vocabulary.
-template <int MODE, typename TT, int FLAGS>
+// A row of zeros standing in for the dense Markov addend when there is none, so the
+// epilogue's addend loads and adds need no branch (the widest read is 512 bytes).
+// (Not const: in the global address space like the addend, so the loads stay global.)
+__device__ uint4 kZeroRow[64] = {};
+
+template <int MODE, typename TT, int FLAGS, bool FULL>
 __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, int half, int64_t t0, int64_t v0) {
   // the teacher is read in pass 2, and in pass 1 unless its log-normaliser is given
   constexpr bool kReadU = MODE == MODE_EMIT || (MODE == MODE_STATS && !(FLAGS & kTeacherLse));
@@ -652,37 +657,67 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
       reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(lds + kLabelOff);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r8 = lane >> 3, c8 = lane & 7;
+  const bool has_m = p.markov != nullptr;   // kernel argument: uniform
+  // FULL: the tile holds no entry past the vocabulary, so nothing is masked
+  // this lane's chunks (the same in every group): loads are unconditional (chunks past V
+  // re-read the row's first chunk) and the values are masked afterwards
+  bool ok[4];
+  int vc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int vl = 8 * c8 + 64 * k;
+    ok[k] = v0 + vl < p.v;
+    vc[k] = ok[k] ? vl : 0;
+  }
+  // the Markov and teacher rows of group g's token: issued one group ahead, so two
+  // groups' loads are in flight while a group is processed
+  auto mrow_of = [&](int g) -> const uint16_t* {
+    const int64_t t = t0 + half * 128 + 32 * w + 8 * g + r8;
+    const int64_t trow = t < p.n ? t : p.n - 1;
+    return has_m ? p.markov + trow * p.ldm + v0 : reinterpret_cast<const uint16_t*>(kZeroRow);
+  };
+  auto urow_of = [&](int g) -> const TT* {
+    const int tk = half * 128 + 32 * w + 8 * g + r8;
+    const int trw = reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk];
+    return kReadU ? static_cast<const TT*>(p.teacher) + (int64_t)trw * p.ldt + v0 : nullptr;
+  };
+  // two statically indexed buffers (the group loop is unrolled), so no copy of a
+  // loaded register forces its wait early
+  Raw8<uint16_t> mbuf[2][4];
+  Raw8<TT> ubuf[2][4];
+  auto issue = [&](int g, int b) {
+    const uint16_t* mr = mrow_of(g);
+    const TT* ur = urow_of(g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (kReadU) ubuf[b][k].load(ur + vc[k]);
+      mbuf[b][k].load(mr + vc[k]);
+    }
+  };
+  // prefetch where the registers allow it (bf16 teacher; not the teacher-once pass 2,
+  // which also carries the KL sum): otherwise each group issues its own loads first
+  constexpr bool kPrefetch = sizeof(TT) == 2 && !(MODE == MODE_EMIT && (FLAGS & kTeacherLse));
+  if (kPrefetch) issue(0, 0);
+  // pairs of groups in a rolled loop: buffer 0 always holds the even group and buffer 1
+  // the odd one, so the loop carries the prefetch in the same registers
 #pragma unroll 1
-  for (int g = 0; g < 4; ++g) {
+  for (int g2 = 0; g2 < 4; g2 += 2)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int g = g2 + j;                    // group; its buffer is j (g2 is even)
     const int tl = 32 * w + 8 * g + r8;      // token within the half
     const int tk = half * 128 + tl;          // token within the workgroup tile
     const int64_t t = t0 + tk;
     const bool tok_ok = t < p.n;
-    const int64_t trow = tok_ok ? t : p.n - 1;
     const lds_f32* zr = zt + tl * kZRow;
-    const bool has_m = p.markov != nullptr;   // kernel argument: uniform, so no divergent branch
-    const uint16_t* mrow = (has_m ? p.markov : p.weight) + (has_m ? trow * p.ldm + v0 : 0);
-    const int trw = reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk];
+    const uint16_t* mrow = mrow_of(g);
     const bool ubad = reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kTbadOff)[tk];
-    const TT* urow = kReadU ? static_cast<const TT*>(p.teacher) + (int64_t)trw * p.ldt + v0 : nullptr;
+    const TT* urow = urow_of(g);
     float z[32], u[32];
-    bool ok[4];
-    // loads are unconditional (chunks past V re-read the row's first chunk) and the
-    // values are masked afterwards, so all of them are in flight together
-    Raw8<uint16_t> mraw[4];
-    Raw8<TT> uraw[4];
-    int vc[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int vl = 8 * c8 + 64 * k;
-      ok[k] = v0 + vl < p.v;
-      vc[k] = ok[k] ? vl : 0;
-      if (kReadU) uraw[k].load(urow + vc[k]);
-    }
-    if (has_m) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) mraw[k].load(mrow + vc[k]);
-    }
+    if (!kPrefetch) issue(g, j);
+    else if (g < 3) issue(g + 1, j ^ 1);
+    const Raw8<uint16_t>(&mraw)[4] = mbuf[j];
+    const Raw8<TT>(&uraw)[4] = ubuf[j];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int vl = 8 * c8 + 64 * k;
@@ -691,25 +726,32 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
 #pragma unroll
       for (int e = 0; e < 4; ++e) { z[8 * k + e] = x0[e]; z[8 * k + 4 + e] = x1[e]; }
     }
-    // a previous-token id outside [0, V) has no Markov row: its logits become NaN, so the
-    // loss reports the bad input (the reference's embedding lookup raises)
-    const bool bad = p.r > 0 && reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tk];
+    // A previous-token id outside [0, V) has no Markov row and a teacher row outside the
+    // teacher tensor has no logits: the row's pass-1 state is made NaN (below), so its
+    // log-normaliser, loss terms and pass-2 dl and accept rate are NaN and the loss reports
+    // the bad input (the reference's embedding lookup and gather raise).
+    const bool bad = reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tk] != 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float mk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (has_m) mraw[k].unpack(mk);
-      if (bad) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) mk[e] = __builtin_nanf("");
-      }
+      float mk[8];
+      mraw[k].unpack(mk);
       if (kReadU) uraw[k].unpack(u + 8 * k);
+      if (MODE == MODE_STORE) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // a gathered B row (MODE_STORE) outside its matrix: the output row is NaN
-        const float zk = MODE == MODE_STORE && ubad ? __builtin_nanf("") : z[8 * k + e] + mk[e];
-        z[8 * k + e] = ok[k] ? zk : kNegBig;
-        // a teacher row outside the teacher tensor: NaN (the reference's gather raises)
-        if (kReadU) u[8 * k + e] = ok[k] ? (ubad ? __builtin_nanf("") : u[8 * k + e]) : kNegBig;
+        for (int e = 0; e < 8; ++e) {
+          // a gathered B row outside its matrix: the output row is NaN
+          const float zk = ubad ? __builtin_nanf("") : z[8 * k + e] + mk[e];
+          z[8 * k + e] = ok[k] ? zk : kNegBig;
+        }
+      } else if (FULL) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) z[8 * k + e] += mk[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          z[8 * k + e] = ok[k] ? z[8 * k + e] + mk[e] : kNegBig;
+          if (kReadU) u[8 * k + e] = ok[k] ? u[8 * k + e] : kNegBig;
+        }
       }
     }
     if (MODE == MODE_STORE) {
@@ -735,28 +777,32 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
     const int64_t yr = y - v0;
     // this lane holds z_y (labels outside [0, V) match nothing; the merge flags them)
     const bool mine = yr >= 0 && yr < BM && y < p.v && ((yr >> 3) & 7) == c8 && tok_ok;
+    const float nan = __builtin_nanf("");
     if (MODE == MODE_STATS && (FLAGS & kTeacherLse)) {
       LseState loc = {kNegBig, 0.f};
-      if (ok[0]) lse_update<32>(loc, z);
+      if (FULL || ok[0]) lse_update<32>(loc, z);
       loc = lse_reduce8(loc);
+      if (bad) loc = {nan, nan};
       if (c8 == 0) {
         lds_f32* sr = state + tk * 8;
         const LseState r = lse_merge(LseState{sr[0], sr[1]}, loc);
         sr[0] = r.m; sr[1] = r.s;
       }
-      if (mine) p.zy[t] = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
+      if (mine) p.zy[t] = bad ? nan : zr[yr] + bf16_to_f32(mrow[yr]);   // rare: the label is in this tile
     } else if (MODE == MODE_STATS) {
       PairState loc = pair_init();
       // ok[] falls with k: a lane with no valid chunk keeps the empty state (an update
       // with every entry at the sentinel would form inf - inf)
-      if (ok[0]) pair_update<32>(loc, z, u);
+      if (FULL || ok[0]) pair_update<32>(loc, z, u);
       loc = pair_reduce8(loc);
+      if (bad) { loc.mz = nan; loc.sz = nan; }
+      if (ubad) { loc.mu = nan; loc.su = nan; loc.A = nan; }
       if (c8 == 0) {
         lds_f32* sr = state + tk * 8;
         const PairState r = pair_merge(PairState{sr[0], sr[1], sr[2], sr[3], sr[4]}, loc);
         sr[0] = r.mz; sr[1] = r.sz; sr[2] = r.mu; sr[3] = r.su; sr[4] = r.A;
       }
-      if (mine) p.zy[t] = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
+      if (mine) p.zy[t] = bad ? nan : zr[yr] + bf16_to_f32(mrow[yr]);   // rare: the label is in this tile
     } else {
       const lds_f32* cr = cst + tk * 8;
       const float lzl = cr[0], lul = cr[1], cp = cr[2], ct = cr[3], cy = cr[4];
@@ -782,9 +828,9 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
         if (c8 == 0) state[tk * 8 + 1] += kloc;
       }
       // the label entry: rewrite dl[y] with the -c_ce term (same lane, after its store)
-      if (mine && p.dl) {
-        const float zy = zr[yr] + (has_m ? bf16_to_f32(mrow[yr]) : 0.f);
-        const float uy = ubad ? __builtin_nanf("") : load1(urow + yr);
+      if (mine && p.dl) {   // rare: the label is in this tile (a bad row's NaN comes through its lse)
+        const float zy = zr[yr] + bf16_to_f32(mrow[yr]);
+        const float uy = load1(urow + yr);
         const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
         const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
         store1(p.dl + t * p.ldd + y, __builtin_fmaf(cp, pp, -ct * tt) - cy);
@@ -814,6 +860,8 @@ void head_kernel(HeadParams p) {
     const bool ok = id >= 0 && id < p.v;
     reinterpret_cast<__attribute__((address_space(3))) int*>(lds + kPrevOff)[tid] = ok ? (int)id : 0;
     reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tid] = ok ? 0 : 1;
+  } else {
+    reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tid] = 0;
   }
   {
     // teacher row (MODE_STORE: gathered B row) of token tid, checked against its tensor
@@ -880,7 +928,10 @@ void head_kernel(HeadParams p) {
     for (int jj = 0; jj < 2; ++jj) {
       if (wn == jj) dump_half(acc, lds);
       __syncthreads();
-      epilogue_half<MODE, TT, FLAGS>(p, lds, jj, t0, v0);
+      if (v0 + BM <= p.v)
+        epilogue_half<MODE, TT, FLAGS, true>(p, lds, jj, t0, v0);
+      else
+        epilogue_half<MODE, TT, FLAGS, false>(p, lds, jj, t0, v0);
       __syncthreads();
     }
   }

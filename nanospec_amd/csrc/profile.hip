@@ -15,6 +15,7 @@ namespace {
 struct Record {
   const char* name;
   hipEvent_t start, stop;
+  hipError_t err;   // a failed stop record: reported by ns_profile_end
 };
 
 std::mutex g_mu;
@@ -40,9 +41,12 @@ bool profiling() { return g_on; }
 void* profile_start(const char* name, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!g_on) return nullptr;
-  Record r{name, take_event(), take_event()};
-  if (!r.start || !r.stop) return nullptr;
-  hipEventRecord(r.start, st);
+  Record r{name, take_event(), take_event(), hipSuccess};
+  if (!r.start || !r.stop || hipEventRecord(r.start, st) != hipSuccess) {
+    if (r.start) g_pool.push_back(r.start);
+    if (r.stop) g_pool.push_back(r.stop);
+    return nullptr;   // this launch goes untimed
+  }
   g_records.push_back(r);
   return reinterpret_cast<void*>(g_records.size());
 }
@@ -51,7 +55,7 @@ void profile_stop(void* token, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!token) return;
   const size_t i = reinterpret_cast<size_t>(token) - 1;
-  if (i < g_records.size()) hipEventRecord(g_records[i].stop, st);
+  if (i < g_records.size()) g_records[i].err = hipEventRecord(g_records[i].stop, st);
 }
 
 }  // namespace ns
@@ -72,7 +76,8 @@ int ns_profile_end(ns_kernel_time* out, int capacity, int* count) {
   int status = NS_OK;
   for (auto& r : ns::g_records) {
     float ms = 0.f;
-    hipError_t e = hipEventSynchronize(r.stop);
+    hipError_t e = r.err;
+    if (e == hipSuccess) e = hipEventSynchronize(r.stop);
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.stop);
     if (e != hipSuccess && status == NS_OK) status = (int)e;
     size_t j = 0;
