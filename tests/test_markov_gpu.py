@@ -44,6 +44,7 @@ def _oracle(hidden, weight, teacher, slots, mk, o):
 @pytest.mark.parametrize("n,d,v,r", [
     (72, 128, 8200, 64),      # partial token and vocab tiles, one Markov K stage
     (256, 256, 4096, 256),    # the reference rank
+    (128, 128, 2048, 512),    # eight Markov K stages
 ])
 def test_markov_forward_matches_oracle(gpu_lib, n, d, v, r):
     hidden, weight, teacher, slots, mk = _inputs(n, d, v, r, 40 + n)
@@ -139,6 +140,8 @@ def _assert_grads(dl, mk, g1, w1_grad, w2_grad, keep=None):
     (256, 4096, 256, 256, None),      # the reference rank, whole stages only
     (1000, 2048, 192, 128, 16),       # long runs of repeated ids (index_add_ segments of ~60)
     (1536, 16384, 256, 256, None),    # 24 token stages, 64 vocab tiles
+    (40, 4096, 128, 64, None),        # fewer tokens than one stage: the register path alone
+    (128, 2048, 128, 512, 8),         # rank 512: two rank tiles in the w2.grad GEMM
 ])
 def test_markov_backward_matches_oracle(gpu_lib, n, v, d, r, id_range):
     dl, w, mk, g1 = _bwd_inputs(n, v, d, r, 60 + n, id_range)
