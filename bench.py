@@ -314,7 +314,8 @@ def workload_head(device, args, which):
 
         from oracle import objective_ref as ref
 
-        rows = rows or 1024
+        # about 10 s of host work at C2 / C4 (whole blocks of 8)
+        rows = rows or (1024 if fp8 is not None else 2560)
         t_copy = time.perf_counter()
         w32 = weight.float().cpu().numpy()
         hs = hidden[:rows].float().cpu().numpy()
@@ -415,7 +416,7 @@ def workload_c2x(device, args):
 
         from oracle import objective_ref as ref
 
-        rows = rows or 1024
+        rows = rows or 2048   # about 10 s of host work
         t_copy = time.perf_counter()
         w32 = weight.float().cpu().numpy()
         w1n, w2n = w1.float().cpu().numpy(), w2.float().cpu().numpy()

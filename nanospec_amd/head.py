@@ -342,13 +342,15 @@ def lm_head_linear(x, lm_head_weight, addend=None):
 
 @torch.no_grad()
 def head_step(hidden, lm_head_weight, target_logits, prepared, objective, *, markov_logits=None,
-              markov=None, markov_grads=None, accumulation_steps=1):
+              markov=None, markov_grads=None, final_norm=None, accumulation_steps=1):
     """The head region of train() (train.py:268-312) on the fused path: returns
     (LossMetrics, dh, dl); dl feeds the Markov-head backward (train.py:303-307).
     With ``markov`` factors and ``markov_grads=(w1_grad, w2_grad)`` that backward runs
-    here too, and the gradient buffers are updated in place."""
+    here too, and the gradient buffers are updated in place.  With ``final_norm``
+    (RMSActivations, norm weight, norm weight grad) the second value is dx, not dh."""
     metrics, saved = lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objective,
                                         markov_logits=markov_logits, markov=markov,
                                         accumulation_steps=accumulation_steps)
-    dh, dl = lm_head_ce_kl_backward(saved, accumulation_steps, return_dlogits=True, markov_grads=markov_grads)
+    dh, dl = lm_head_ce_kl_backward(saved, accumulation_steps, return_dlogits=True, markov_grads=markov_grads,
+                                    final_norm=final_norm)
     return metrics, dh, dl
