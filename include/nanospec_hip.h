@@ -7,6 +7,9 @@
  *   nanospec/objective.py:39-46   acceptance_length_counts (inside both fwd entries)
  *   nanospec/ops.py:34-35 via train.py:272-279, 291   linear + ce_kl_loss fused
  *                                                     -> ns_lmhead_ce_kl_fwd
+ *   nanospec/objective.py:70-80 via train.py:301  ce_kl_backward after the fused
+ *                                 forward (dl for the backward's accumulation_steps)
+ *                                                     -> ns_lmhead_ce_kl_bwd
  *   nanospec/train.py:302         dh = dl @ lm_head.w -> ns_lmhead_bwd
  *   nanospec/train.py:276-279 (MarkovHead, layers.py:74-78: embedding + linear)
  *     fused into the LM head as a second K segment -> ns_lmhead_markov_ce_kl_fwd
@@ -44,7 +47,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 4
+#define NS_ABI_VERSION 5
 
 #define NS_BF16 0
 #define NS_F32 1
@@ -147,6 +150,21 @@ int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weig
                                int64_t d, int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl,
                                int64_t ldd, float* row_stats, float* metrics, void* workspace,
                                size_t workspace_bytes, ns_stream_t stream);
+
+/* dl alone for the fused head: ce_kl_backward (objective.py:70-80) as train.py:301 calls it,
+ * with the backward's accumulation_steps (inv_acc = 1/accumulation_steps).  Runs pass 2 of
+ * ns_lmhead_ce_kl_fwd / ns_lmhead_markov_ce_kl_fwd again over the same inputs, reading the
+ * row log-normalisers from the row_stats that forward wrote: the same kernel, so dl holds
+ * the bits a forward called with this inv_acc emits.  Markov head as in that forward:
+ * markov [N, V] bf16 (dense addend), or prev, w1, w2 with r > 0 (factors), or neither
+ * (markov NULL, r == 0).  dl [N, V] bf16 is required.  dh follows from dl through
+ * ns_lmhead_bwd, ns_lmhead_markov_bwd or ns_lmhead_norm_bwd.  Workspace NS_WS_LMHEAD. */
+int ns_lmhead_ce_kl_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                        int64_t ldm, const int64_t* prev, const void* w1, int64_t ldw1, const void* w2, int64_t ldw2,
+                        int64_t r, const void* teacher, int t_dtype, int64_t ldt, const ns_teacher_args* teacher_args,
+                        const int64_t* labels, const float* weights, int64_t n, int64_t d, int64_t v, float c_ce,
+                        float c_kl, float inv_acc, const float* row_stats, void* dl, int64_t ldd, void* workspace,
+                        size_t workspace_bytes, ns_stream_t stream);
 
 /* Teacher-logit producer (train.py:172-173 and 281-284: ops.linear of the teacher's last
  * hidden state, gathered at teacher_indices, by the shared LM head):

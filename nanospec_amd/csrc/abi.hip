@@ -146,18 +146,19 @@ int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, 
 
 namespace {
 
-// Shared validation and launch of the fused forward (dense Markov addend or factors).
-int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
-                       int64_t ldm, const ns::MarkovFactors* factors, const void* teacher, int t_dtype, int64_t ldt,
-                       const ns_teacher_args* targs, const int64_t* labels, const float* weights, const uint8_t* valid, int64_t n, int64_t d,
-                       int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl, int64_t ldd,
-                       float* row_stats, float* metrics, void* workspace, size_t workspace_bytes,
-                       ns_stream_t stream, const char* name) {
+// Validation shared by the fused forward and the dl re-emission (dense Markov addend or
+// factors).  `reemit`: dl is required, row_stats is an input, metrics and valid are unused.
+int check_head_inputs(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                      int64_t ldm, const ns::MarkovFactors* factors, const void* teacher, int t_dtype, int64_t ldt,
+                      const ns_teacher_args* targs, const int64_t* labels, const float* weights,
+                      const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k, const void* dl, int64_t ldd,
+                      const float* row_stats, const float* metrics, const void* workspace, size_t workspace_bytes,
+                      bool reemit, int64_t* nt_out) {
   if (!dtype_ok(t_dtype)) return fail(NS_EDTYPE, "unsupported teacher dtype code %d", t_dtype);
   if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
   if (d < 64 || d % 64) return fail(NS_EINVAL, "hidden size must be a positive multiple of 64 (got %lld)", (long long)d);
   int rc;
-  if ((rc = check_slots(labels, weights, valid, n, k, true))) return rc;
+  if ((rc = check_slots(labels, weights, valid, n, k, !reemit))) return rc;
   if ((rc = check_matrix(hidden, n, d, ldh, "hidden"))) return rc;
   if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
   if (markov && (rc = check_matrix(markov, n, v, ldm, "markov"))) return rc;
@@ -168,8 +169,9 @@ int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int6
   if (targs && n > 0 && targs->n_rows > 0 && !targs->rows && targs->n_rows != n)
     return fail(NS_EINVAL, "teacher n_rows %lld without rows must equal n", (long long)targs->n_rows);
   if ((rc = check_matrix(teacher, nt, v, ldt, "teacher"))) return rc;
-  if (dl && (rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
-  if (!metrics || (n > 0 && !row_stats)) return fail(NS_ENULL, "metrics and row_stats must be non-NULL");
+  if ((reemit || dl) && (rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
+  if (reemit ? (n > 0 && !row_stats) : (!metrics || (n > 0 && !row_stats)))
+    return fail(NS_ENULL, reemit ? "row_stats must be non-NULL" : "metrics and row_stats must be non-NULL");
   const int64_t tq = t_dtype == NS_BF16 ? 8 : 4;
   if (!aligned(hidden) || !aligned(weight) || !aligned(teacher) || (markov && !aligned(markov)) || (dl && !aligned(dl)) ||
       ldh % 8 || ldw % 8 || (markov && ldm % 8) || ldt % tq || (dl && ldd % 8))
@@ -190,6 +192,21 @@ int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int6
   if (n > 0 && (!workspace || workspace_bytes < need))
     return fail(NS_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return fail(NS_EALIGN, "workspace must be 256-byte aligned");
+  *nt_out = nt;
+  return 0;
+}
+
+int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                       int64_t ldm, const ns::MarkovFactors* factors, const void* teacher, int t_dtype, int64_t ldt,
+                       const ns_teacher_args* targs, const int64_t* labels, const float* weights, const uint8_t* valid,
+                       int64_t n, int64_t d, int64_t v, int64_t k, float c_ce, float c_kl, float inv_acc, void* dl,
+                       int64_t ldd, float* row_stats, float* metrics, void* workspace, size_t workspace_bytes,
+                       ns_stream_t stream, const char* name) {
+  int64_t nt = 0;
+  const int rc = check_head_inputs(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, targs, labels,
+                                   weights, valid, n, d, v, k, dl, ldd, row_stats, metrics, workspace, workspace_bytes,
+                                   false, &nt);
+  if (rc) return rc;
   ns::SlotArgs a{labels, weights, valid, n, k, c_ce, c_kl, inv_acc};
   const ns::TeacherSpec ts{targs ? targs->rows : nullptr, nt, targs ? targs->lse : nullptr};
   return hip_status(ns::lmhead_forward(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, d, v,
@@ -224,6 +241,29 @@ int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weig
   return lmhead_fwd_checked(hidden, ldh, weight, ldw, nullptr, 0, &f, teacher, t_dtype, ldt, teacher_args, labels,
                             weights, valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, workspace,
                             workspace_bytes, stream, "ns_lmhead_markov_ce_kl_fwd");
+}
+
+int ns_lmhead_ce_kl_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                        int64_t ldm, const int64_t* prev, const void* w1, int64_t ldw1, const void* w2, int64_t ldw2,
+                        int64_t r, const void* teacher, int t_dtype, int64_t ldt, const ns_teacher_args* teacher_args,
+                        const int64_t* labels, const float* weights, int64_t n, int64_t d, int64_t v, float c_ce,
+                        float c_kl, float inv_acc, const float* row_stats, void* dl, int64_t ldd, void* workspace,
+                        size_t workspace_bytes, ns_stream_t stream) {
+  if (markov && r != 0) return fail(NS_EINVAL, "pass either a dense Markov addend or factors (r > 0), not both");
+  if (r < 0) return fail(NS_EINVAL, "Markov rank must be >= 0 (got %lld)", (long long)r);
+  const ns::MarkovFactors f{prev, w1, w2, ldw1, ldw2, r};
+  const ns::MarkovFactors* factors = r > 0 ? &f : nullptr;
+  int64_t nt = 0;
+  const int rc = check_head_inputs(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, teacher_args,
+                                   labels, weights, nullptr, n, d, v, 1, dl, ldd, row_stats, nullptr, workspace,
+                                   workspace_bytes, true, &nt);
+  if (rc) return rc;
+  ns::SlotArgs a{labels, weights, nullptr, n, 1, c_ce, c_kl, inv_acc};
+  const ns::TeacherSpec ts{teacher_args ? teacher_args->rows : nullptr, nt, teacher_args ? teacher_args->lse : nullptr};
+  return hip_status(ns::lmhead_emit_dlogits(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, d,
+                                            v, a, &ts, row_stats, dl, ldd, workspace,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                    "ns_lmhead_ce_kl_bwd");
 }
 
 int ns_lmhead_teacher_logits(const void* x, int64_t ldx, const int64_t* rows, int64_t n_rows, const void* weight,

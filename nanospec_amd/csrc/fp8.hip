@@ -387,7 +387,7 @@ Fp8Plan fp8_plan(int64_t n, int64_t v) {
   int cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  int sp = (cus + pl.tt - 1) / pl.tt;
+  int sp = pl.tt > 0 ? (cus + pl.tt - 1) / pl.tt : 1;   // no rows: nothing launches
   sp = sp < 1 ? 1 : (sp > pl.vt ? pl.vt : sp);
   pl.splits = sp;
   pl.xa = xcd_block(pl.tt, sp);

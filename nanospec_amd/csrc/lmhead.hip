@@ -1102,7 +1102,7 @@ HeadPlan head_plan(int64_t n, int64_t v) {
   pl.tt = (int)((n + BN - 1) / BN);
   pl.vt = (int)((v + BM - 1) / BM);
   const int cus = device_cus();
-  int s = (cus + pl.tt - 1) / pl.tt;
+  int s = pl.tt > 0 ? (cus + pl.tt - 1) / pl.tt : 1;   // no rows: nothing launches
   if (s < 1) s = 1;
   if (s > pl.vt) s = pl.vt;
   pl.splits = s;
@@ -1147,7 +1147,7 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   pl.kt_total = (int)((v + BK - 1) / BK);
   const int tiles = pl.mt * pl.ct;
   const int cus = device_cus();
-  int ks = (4 * cus + tiles - 1) / tiles;
+  int ks = tiles > 0 ? (4 * cus + tiles - 1) / tiles : 1;   // no tiles: nothing launches
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
   if (ks > pl.kt_total) ks = pl.kt_total;
@@ -1159,7 +1159,7 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   pl.grid = pl.grid_main;
   if (pl.ct2 > 0) {
     const int tiles2 = pl.mt * pl.ct2;
-    int ks2 = (cus + tiles2 - 1) / tiles2;
+    int ks2 = tiles2 > 0 ? (cus + tiles2 - 1) / tiles2 : 1;
     if (ks2 < ks) ks2 = ks;
     if (ks2 > 64) ks2 = 64;
     if (ks2 > pl.kt_total) ks2 = pl.kt_total;
@@ -1214,14 +1214,13 @@ size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d) {
   return head_ws_layout(n, v, nullptr, nullptr);
 }
 
-hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
-                          int64_t ldm, const MarkovFactors* factors, const void* teacher, int tdt, int64_t ldt,
-                          int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts, void* dl, int64_t ldd,
-                          float* row_stats, float* metrics, void* ws, hipStream_t st) {
-  if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
-  const HeadPlan pl = head_plan(a.n, v);
-  HeadWs w;
-  head_ws_layout(a.n, v, ws, &w);
+namespace {
+
+// The fused head's kernel arguments, shared by the forward and the dl re-emission.
+HeadParams head_params(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                       int64_t ldm, const MarkovFactors* factors, const void* teacher, int64_t ldt, int64_t d,
+                       int64_t v, const SlotArgs& a, const TeacherSpec* ts, void* dl, int64_t ldd,
+                       const HeadPlan& pl, const HeadWs& w) {
   HeadParams p = {};
   p.hidden = static_cast<const uint16_t*>(hidden);
   p.weight = static_cast<const uint16_t*>(weight);
@@ -1243,12 +1242,46 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
     p.w2 = static_cast<const uint16_t*>(factors->w2);
     p.ldw1 = factors->ldw1; p.ldw2 = factors->ldw2; p.r = factors->r;
   }
+  return p;
+}
+
+}  // namespace
+
+hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                          int64_t ldm, const MarkovFactors* factors, const void* teacher, int tdt, int64_t ldt,
+                          int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts, void* dl, int64_t ldd,
+                          float* row_stats, float* metrics, void* ws, hipStream_t st) {
+  if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
+  const HeadPlan pl = head_plan(a.n, v);
+  HeadWs w;
+  head_ws_layout(a.n, v, ws, &w);
+  HeadParams p = head_params(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, ldt, d, v, a, ts, dl, ldd, pl, w);
   if (p.tlse) {
     if (tdt == kBF16) return head_forward_typed<uint16_t, kTeacherLse>(p, pl, a, row_stats, metrics, w, st);
     return head_forward_typed<float, kTeacherLse>(p, pl, a, row_stats, metrics, w, st);
   }
   if (tdt == kBF16) return head_forward_typed<uint16_t, 0>(p, pl, a, row_stats, metrics, w, st);
   return head_forward_typed<float, 0>(p, pl, a, row_stats, metrics, w, st);
+}
+
+hipError_t lmhead_emit_dlogits(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                               int64_t ldm, const MarkovFactors* factors, const void* teacher, int tdt, int64_t ldt,
+                               int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts,
+                               const float* row_stats, void* dl, int64_t ldd, void* ws, hipStream_t st) {
+  if (a.n == 0) return hipSuccess;
+  const HeadPlan pl = head_plan(a.n, v);
+  HeadWs w;
+  head_ws_layout(a.n, v, ws, &w);
+  HeadParams p = head_params(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, ldt, d, v, a, ts, dl, ldd, pl, w);
+  // pass 2 alone: the row log-normalisers come from the forward's row_stats, the accept
+  // and KL partials it also forms go to the workspace and are not read
+  p.row_stats = row_stats;
+  if (p.tlse) {
+    if (tdt == kBF16) return launch_head<MODE_EMIT, uint16_t, kTeacherLse>(p, pl.grid, st, "head_emit");
+    return launch_head<MODE_EMIT, float, kTeacherLse>(p, pl.grid, st, "head_emit");
+  }
+  if (tdt == kBF16) return launch_head<MODE_EMIT, uint16_t, 0>(p, pl.grid, st, "head_emit");
+  return launch_head<MODE_EMIT, float, 0>(p, pl.grid, st, "head_emit");
 }
 
 size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r, bool norm) {

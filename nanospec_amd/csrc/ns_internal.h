@@ -85,6 +85,14 @@ hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, i
                           const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
                           int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts,
                           void* dl, int64_t ldd, float* row_stats, float* metrics, void* ws, hipStream_t st);
+// Pass 2 of lmhead_forward alone: dl for a.inv_acc from the row_stats a forward over the
+// same inputs wrote (same kernel, so the same bits a forward with that inv_acc emits).
+// Workspace: lmhead_workspace_bytes.
+hipError_t lmhead_emit_dlogits(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                               const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
+                               int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a,
+                               const TeacherSpec* ts, const float* row_stats, void* dl, int64_t ldd, void* ws,
+                               hipStream_t st);
 // dh workspace; r > 0 adds the Markov column tiles' partials, norm the rms-norm
 // backward's column partials
 size_t lmhead_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t r = 0, bool norm = false);

@@ -90,9 +90,30 @@ def teacher_logits(x, lm_head_weight, rows=None):
 
 
 @dataclass
+class _HeadInputs:
+    """The fused forward's operands as [rows, cols] views of the caller's tensors (no
+    copies), kept so the backward can run pass 2 again for another accumulation_steps."""
+
+    h: torch.Tensor
+    ldh: int
+    w: torch.Tensor
+    ldw: int
+    m: torch.Tensor | None
+    ldm: int
+    factors: tuple | None      # (prev, w1, ldw1, w2, ldw2, r)
+    u: torch.Tensor
+    ldu: int
+    rows: torch.Tensor | None
+    lse: torch.Tensor | None
+    labels: torch.Tensor
+    weights: torch.Tensor
+
+
+@dataclass
 class HeadActivations:
-    """State the fused backward needs: per-row statistics, the emitted dl and the
-    frozen head weight.  row_stats [N, 8] = (lse_z, lse_u, ce, kl, accept_rate, z_label, 0, 0)."""
+    """State the fused backward needs: per-row statistics, the emitted dl, the frozen head
+    weight and references to the forward's inputs.  row_stats [N, 8] = (lse_z, lse_u, ce,
+    kl, accept_rate, z_label, 0, 0)."""
 
     objective: Objective
     weight: torch.Tensor
@@ -101,6 +122,7 @@ class HeadActivations:
     accumulation_steps: int
     shape: tuple
     markov: MarkovFactors | None = None
+    inputs: _HeadInputs | None = None
 
 
 def _bf16_rows(t: torch.Tensor, cols: int, name: str):
@@ -117,8 +139,9 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
     hidden [..., K, d] bf16; lm_head_weight [V, d] bf16; target_logits [..., K, V]
     bf16 or fp32, or a ``TeacherLogits`` (teacher rows gathered in the loads, and the
     producer's log-normalisers); markov_logits [..., K, V] bf16 or None; prepared has weights,
-    target_ids, valid [..., K].  dl is emitted for ``accumulation_steps`` (pass the
-    same value to the backward).  ``markov`` (a ``MarkovFactors``) adds the Markov
+    target_ids, valid [..., K].  dl is emitted for ``accumulation_steps`` (a backward
+    with another value, or after ``emit_dlogits=False``, runs pass 2 again).  ``saved``
+    keeps references to these inputs for that.  ``markov`` (a ``MarkovFactors``) adds the Markov
     head in factored form instead of a dense ``markov_logits`` tensor: it is fused
     into the GEMM as a second K segment, and the backward can form its gradients.
     """
@@ -160,21 +183,50 @@ def lm_head_ce_kl_loss(hidden, lm_head_weight, target_logits, prepared, objectiv
     row_stats = torch.empty((n, 8), dtype=torch.float32, device=device)
     dl = torch.empty((n, vocab), dtype=torch.bfloat16, device=device) if emit_dlogits else None
     ws = _lib.workspace(_lib.NS_WS_LMHEAD, n, vocab, d, device)
-    tail = (_lib.ptr(u), _lib.dtype_code(u), ldu, ctypes.byref(targs) if targs is not None else None, _lib.ptr(y), _lib.ptr(wts), _lib.ptr(valid), n, d, vocab, k,
-            float(o.ce), float(o.kl), 1.0 / accumulation_steps, _lib.ptr(dl), vocab, _lib.ptr(row_stats),
-            _lib.ptr(metrics), _lib.ptr(ws), ws.numel(), _lib.stream(device))
+    tail = (_lib.ptr(u), _lib.dtype_code(u), ldu, ctypes.byref(targs) if targs is not None else None, _lib.ptr(y),
+            _lib.ptr(wts), _lib.ptr(valid), n, d, vocab, k, float(o.ce), float(o.kl), 1.0 / accumulation_steps,
+            _lib.ptr(dl), vocab, _lib.ptr(row_stats), _lib.ptr(metrics), _lib.ptr(ws), ws.numel(),
+            _lib.stream(device))
+    factors = None
     if markov is None:
         status = lib.ns_lmhead_ce_kl_fwd(_lib.ptr(h), ldh, _lib.ptr(w), ldw, _lib.ptr(m), ldm, *tail)
         _lib.check(status, "ns_lmhead_ce_kl_fwd")
     else:
-        prev, w1, ldw1, w2, ldw2, r = _markov_inputs(markov, vocab, n, device)
+        factors = _markov_inputs(markov, vocab, n, device)
+        prev, w1, ldw1, w2, ldw2, r = factors
         status = lib.ns_lmhead_markov_ce_kl_fwd(_lib.ptr(h), ldh, _lib.ptr(w), ldw, _lib.ptr(prev), _lib.ptr(w1),
                                                 ldw1, _lib.ptr(w2), ldw2, r, *tail)
         _lib.check(status, "ns_lmhead_markov_ce_kl_fwd")
+    inputs = _HeadInputs(h, ldh, w, ldw, m, ldm, factors, u, ldu, keep[0] if keep else None,
+                         keep[1] if keep else None, y, wts)
     del keep
     shape = tuple(hidden.shape[:-1]) + (vocab,)
-    saved = HeadActivations(o, lm_head_weight, row_stats, dl, accumulation_steps, shape, markov)
+    saved = HeadActivations(o, lm_head_weight, row_stats, dl, accumulation_steps, shape, markov, inputs)
     return LossMetrics.from_buffer(metrics), saved
+
+
+def _reemit_dlogits(saved: HeadActivations, accumulation_steps: int) -> torch.Tensor:
+    """dl [N, V] bf16 for ``accumulation_steps``: pass 2 of the fused forward again, over the
+    kept inputs and row statistics (ns_lmhead_ce_kl_bwd), the bits a forward with that
+    accumulation_steps emits (objective.py:70-80 as train.py:301 calls it)."""
+    x, o = saved.inputs, saved.objective
+    n = x.h.shape[0]
+    vocab, d = saved.weight.shape
+    device = x.h.device
+    dl = torch.empty((n, vocab), dtype=torch.bfloat16, device=device)
+    ws = _lib.workspace(_lib.NS_WS_LMHEAD, n, vocab, d, device)
+    targs = None
+    if x.rows is not None or x.lse is not None:
+        targs = _lib.TeacherArgs(_lib.ptr(x.rows), x.u.shape[0] if x.rows is not None else 0, _lib.ptr(x.lse))
+    prev, w1, ldw1, w2, ldw2, r = x.factors if x.factors is not None else (None, None, 0, None, 0, 0)
+    status = _lib.load().ns_lmhead_ce_kl_bwd(
+        _lib.ptr(x.h), x.ldh, _lib.ptr(x.w), x.ldw, _lib.ptr(x.m), x.ldm, _lib.ptr(prev), _lib.ptr(w1), ldw1,
+        _lib.ptr(w2), ldw2, r, _lib.ptr(x.u), _lib.dtype_code(x.u), x.ldu,
+        ctypes.byref(targs) if targs is not None else None, _lib.ptr(x.labels), _lib.ptr(x.weights), n, d, vocab,
+        float(o.ce), float(o.kl), 1.0 / accumulation_steps, _lib.ptr(saved.row_stats), _lib.ptr(dl), vocab,
+        _lib.ptr(ws), ws.numel(), _lib.stream(device))
+    _lib.check(status, "ns_lmhead_ce_kl_bwd")
+    return dl
 
 
 def _markov_inputs(markov: MarkovFactors, vocab: int, n: int, device):
@@ -291,20 +343,23 @@ def lm_head_markov_backward(dl, lm_head_weight, markov: MarkovFactors, w1_grad, 
 @torch.no_grad()
 def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, return_dlogits=False,
                            markov_grads=None, final_norm=None):
-    """dh = dl . W_lm with the dl emitted by the forward.  Returns dh [..., d] bf16
-    (and dl [..., V] bf16 when ``return_dlogits``, for the Markov backward).
+    """dh = dl . W_lm (train.py:301-302).  Returns dh [..., d] bf16 (and dl [..., V] bf16
+    when ``return_dlogits``, for the Markov backward).  dl is the one the forward emitted
+    when it was emitted for this ``accumulation_steps``; otherwise (another value,
+    ``emit_dlogits=False``, or a second backward) pass 2 runs again from the saved row
+    statistics, giving the bits a forward with this value emits.
     ``markov_grads=(w1_grad, w2_grad)`` with a factored Markov forward also runs the
     Markov-head backward in the same GEMM (``lm_head_markov_backward``).
     ``final_norm=(RMSActivations, norm weight, norm weight grad)`` fuses final_norm's
     backward into the dh reduction and returns dx in place of dh (train.py:308-310)."""
-    if saved.dlogits is None:
-        raise ValueError("no dl to propagate: the forward ran with emit_dlogits=False, or the backward already ran")
-    if accumulation_steps != saved.accumulation_steps:
-        raise ValueError(
-            f"dl was emitted for accumulation_steps={saved.accumulation_steps}; pass the same value "
-            "to lm_head_ce_kl_loss and lm_head_ce_kl_backward"
-        )
-    dl, saved.dlogits = saved.dlogits, None   # handed over once, so it is freed after dh unless returned
+    if accumulation_steps < 1:
+        raise ValueError("accumulation_steps must be >= 1")
+    if saved.dlogits is not None and accumulation_steps == saved.accumulation_steps:
+        dl = saved.dlogits
+    else:
+        saved.dlogits = None
+        dl = _reemit_dlogits(saved, accumulation_steps)
+    saved.dlogits = None   # handed over once, so it is freed after dh unless returned
     if markov_grads is not None:
         if saved.markov is None:
             raise ValueError("markov_grads given, but the forward ran without Markov factors")

@@ -106,3 +106,50 @@ def test_markov_and_pooled_validation(lib):
         lib.ns_workspace_bytes(_lib.NS_WS_LMHEAD_BWD, 4096, 248320, 5120)
     assert lib.ns_workspace_bytes(_lib.NS_WS_LMHEAD_NORM_BWD, 4096, 248320, 5120) > \
         lib.ns_workspace_bytes(_lib.NS_WS_LMHEAD_BWD, 4096, 248320, 5120)
+
+
+def _head_bwd(lib, **over):
+    """ns_lmhead_ce_kl_bwd with fake (never dereferenced) pointers: n=8, d=64, V=64."""
+    a = dict(hidden=256, ldh=64, weight=256, ldw=64, markov=None, ldm=64, prev=None, w1=None, ldw1=0, w2=None,
+             ldw2=0, r=0, teacher=256, tdt=0, ldt=64, labels=256, weights=256, n=8, d=64, v=64, inv_acc=0.5,
+             row_stats=256, dl=512, ldd=64, ws=256, wsb=1 << 24)
+    a.update(over)
+    p = lambda x: None if x is None else ctypes.c_void_p(x)
+    return lib.ns_lmhead_ce_kl_bwd(
+        p(a["hidden"]), a["ldh"], p(a["weight"]), a["ldw"], p(a["markov"]), a["ldm"], p(a["prev"]), p(a["w1"]),
+        a["ldw1"], p(a["w2"]), a["ldw2"], a["r"], p(a["teacher"]), a["tdt"], a["ldt"], None, p(a["labels"]),
+        p(a["weights"]), a["n"], a["d"], a["v"], 0.1, 0.9, a["inv_acc"], p(a["row_stats"]), p(a["dl"]), a["ldd"],
+        p(a["ws"]), a["wsb"], None)
+
+
+@pytest.mark.parametrize("over,code,text", [
+    (dict(dl=None), -5, "dl is NULL"),                       # the re-emission has no other output
+    (dict(row_stats=None), -5, "row_stats"),                 # it is the input here
+    (dict(markov=256, r=64, prev=256, w1=256, ldw1=64, w2=256, ldw2=64), -1, "not both"),
+    (dict(r=32, prev=256, w1=256, ldw1=64, w2=256, ldw2=64), -1, "Markov rank"),
+    (dict(r=-64), -1, "Markov rank"),
+    (dict(d=96), -1, "hidden size"),
+    (dict(tdt=3), -2, "teacher dtype"),
+    (dict(ldd=60), -1, "leading dimension"),
+    (dict(dl=520), -3, "aligned"),
+    (dict(wsb=16), -4, "workspace"),
+    (dict(labels=None), -5, "non-NULL"),
+])
+def test_lmhead_ce_kl_bwd_validation(lib, over, code, text):
+    assert _head_bwd(lib, **over) == code
+    assert text in lib.ns_last_error().decode()
+
+
+def test_lmhead_ce_kl_bwd_empty(lib):
+    # no rows: nothing to emit, and no pointer is needed
+    assert _head_bwd(lib, n=0, hidden=None, dl=None, row_stats=None, labels=None, weights=None, ws=None,
+                     wsb=0) == 0
+
+
+@pytest.mark.parametrize("kind", range(7))
+@pytest.mark.parametrize("n,v,d", [(0, 248320, 5120), (0, 0, 0), (8, 0, 64), (8, 64, 0)])
+def test_workspace_query_degenerate_shapes(lib, kind, n, v, d):
+    # empty batches and zero-sized dimensions size to a finite workspace (the plans
+    # divide by the number of row and column tiles, which is 0 here)
+    assert lib.ns_workspace_bytes(kind, n, v, d) < 1 << 40
+    assert lib.ns_lmhead_markov_bwd_workspace_bytes(n, v, d, 64) < 1 << 40
