@@ -24,8 +24,20 @@ constexpr int kNumXcd = 8;   // MI355X: 8 XCDs, workgroups dispatched round-robi
 __device__ __forceinline__ int swz(int row) { return ((row & 7) + ((row >> 3) & 1)) & 7; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ swz(row)) << 4); }
 
-// A ROWS-row operand tile (128-byte rows) fetched straight into LDS with
-// global_load_lds_dwordx4.  Each of the 4 waves issues NI = ROWS / 32 instructions per
+// One 16-byte-per-lane fill straight into LDS: lane l's 16 bytes at base + voff land in
+// slot l of the 1 KB block at dst.  Issued as buffer_load_dwordx4 ... lds (a raw buffer
+// over base, offsets < 4 GiB) rather than global_load_lds: the compiler treats a pending
+// FLAT-encoded LDS fill as able to complete out of order with LDS reads, so it waits
+// for every outstanding LDS read (lgkmcnt(0)) before any fragment use; with the buffer
+// form it waits only for the reads a fragment needs.  Same bytes, same LDS layout.
+__device__ __forceinline__ void dma16(const char* base, uint32_t voff, lds_t* dst) {
+  // word 3: 32-bit data format, the raw-buffer setting for gfx9-family descriptors
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, -1, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, reinterpret_cast<__attribute__((address_space(3))) void*>(dst), 16,
+                                           voff, 0, 0, 0);
+}
+
+// A ROWS-row operand tile (128-byte rows) fetched straight into LDS (dma16).  Each of the 4 waves issues NI = ROWS / 32 instructions per
 // stage; instruction i of wave wv fills the 1 KB LDS block wv * NI + i, i.e. rows
 // 8 (wv * NI + i) .. +8.  Lane l writes the block's 16-byte slot l, which is physical
 // chunk l % 8 of row 8 (wv * NI + i) + l / 8; the lane therefore fetches the logical
@@ -62,9 +74,7 @@ struct DmaTile {
   // instruction i of one stage: `base` = the tile's first row at this stage's K offset,
   // `dst` = the operand's LDS stage buffer (wave-uniform)
   __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
-                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * NI + i) * 1024),
-                                     16, 0, 0);
+    dma16(base, off[i], dst + (wv * NI + i) * 1024);
   }
 };
 
@@ -88,9 +98,7 @@ struct DmaTileKN {
     }
   }
   __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + off[i]),
-                                     reinterpret_cast<__attribute__((address_space(3))) void*>(dst + (wv * 8 + i) * 1024),
-                                     16, 0, 0);
+    dma16(base, off[i], dst + (wv * 8 + i) * 1024);
   }
 };
 
@@ -156,16 +164,18 @@ __device__ __forceinline__ void wg_coords(int g, int G, int TT, int xa, int& t, 
 }
 
 // t-tiles per XCD block for a tt x splits grid (wg_coords): a divisor a of C = grid / 8
-// with tt % a == 0 and splits % (C / a) == 0, minimising a + C / a (distinct operand
-// tiles per K stage in one L2); 0 when no such block exists.
-inline int xcd_block(int tt, int splits) {
+// with tt % a == 0 and splits % (C / a) == 0, minimising the distinct operand bytes one
+// L2 serves per K stage, a * t_stage + (C / a) * s_stage (t_stage: one t-tile's operand
+// stage, shared by the block's splits; s_stage: one split's); ties keep the smaller a.
+// 0 when no such block exists.
+inline int xcd_block(int tt, int splits, int64_t t_stage = 1, int64_t s_stage = 1) {
   const int grid = tt * splits;
   if (grid % kNumXcd) return 0;
   const int C = grid / kNumXcd;
   int best = 0;
   for (int a = 1; a <= C; ++a) {
     if (C % a || tt % a || splits % (C / a)) continue;
-    if (best == 0 || a + C / a < best + C / best) best = a;
+    if (best == 0 || a * t_stage + (C / a) * s_stage < best * t_stage + (C / best) * s_stage) best = a;
   }
   return best;
 }
