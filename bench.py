@@ -265,7 +265,9 @@ def workload_c1(device, args):
                 "read2_write1_ms": rw, "read2_write1_GBs": 3 * b / (rw / 1e3) / 1e9}
 
     return dict(step=step, n=n, per_slot_bytes=per_slot, per_slot_flops=None, kernel_bytes=kernel_bytes,
-                kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16", ceilings=ceilings)
+                kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16", ceilings=ceilings,
+                inputs={"draft_logits": z, "teacher_logits": u, "weights": slots.weights,
+                        "target_ids": slots.target_ids, "valid": slots.valid})
 
 
 # --------------------------------------------------------------------------- C2 / C3
@@ -362,7 +364,13 @@ def workload_head(device, args, which):
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d, kernel_bytes=kernel_bytes,
                 kernel_flops=kernel_flops, kernel_fp8_flops=kernel_fp8_flops, cpu_baseline=cpu_baseline,
                 config=config, dtype="bf16" if fp8 is None else "bf16+fp8", ceilings=ceilings,
-                per_slot_fp8_flops=2.0 * v * d if fp8 is not None else None)
+                per_slot_fp8_flops=2.0 * v * d if fp8 is not None else None,
+                inputs={"hidden": hidden, "lm_head_weight": weight, "markov_logits": markov,
+                        "teacher_logits": teacher,
+                        "teacher_hidden": fp8[0] if fp8 is not None else None,
+                        "teacher_head_codes": fp8[1] if fp8 is not None else None,
+                        "teacher_head_scales": fp8[2] if fp8 is not None else None,
+                        "weights": slots.weights, "target_ids": slots.target_ids, "valid": slots.valid})
 
 
 # --------------------------------------------------------------------------- C2X
@@ -452,7 +460,10 @@ def workload_c2x(device, args):
               "parallelism": "single GPU"}
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d + 6.0 * v * r,
                 kernel_bytes=kernel_bytes, kernel_flops=kernel_flops, kernel_fp8_flops={},
-                cpu_baseline=cpu_baseline, config=config, dtype="bf16", per_slot_fp8_flops=None)
+                cpu_baseline=cpu_baseline, config=config, dtype="bf16", per_slot_fp8_flops=None,
+                inputs={"pre_norm_hidden": x, "lm_head_weight": weight, "teacher_logits": teacher,
+                        "previous": prev, "markov_w1": w1, "markov_w2": w2, "weights": slots.weights,
+                        "target_ids": slots.target_ids, "valid": slots.valid})
 
 
 WORKLOADS = {
@@ -462,6 +473,21 @@ WORKLOADS = {
     "c3": lambda dev, a: workload_head(dev, a, "c3"),
     "c4": lambda dev, a: workload_head(dev, a, "c4"),
 }
+
+
+def sample_sha256(t) -> str:
+    """sha256 (first 16 hex digits) of about 64 Ki elements taken at a fixed stride from the
+    flattened tensor: identifies the seeded inputs of a run without hashing gigabytes."""
+    import hashlib
+
+    import torch
+
+    flat = t.reshape(-1)
+    stride = max(1, flat.numel() // 65536)
+    sample = flat[::stride].contiguous().cpu()
+    if sample.dtype == torch.bool:
+        sample = sample.to(torch.uint8)
+    return hashlib.sha256(sample.view(torch.uint8).numpy().tobytes()).hexdigest()[:16]
 
 
 def _time_ms(fn, reps: int = 5) -> float:
@@ -616,6 +642,7 @@ def main():
         "cpu_baseline": cpu,
         "library_ceilings": ceil,
         "wall_s": wall,
+        "inputs_sha256": {k: sample_sha256(t) for k, t in wl.get("inputs", {}).items() if t is not None},
         "host": {"cpu_model": cpu_model(), "cpu_count": os.cpu_count()},
         "device": torch.cuda.get_device_name(device),
     }
