@@ -67,7 +67,8 @@ struct Fp8Params {
   uint16_t* out;           // [N, V] bf16
   int64_t ldo;
   int64_t n, v, d;
-  int tt, vt, splits, xa;  // token tiles, vocab tiles, vocab splits, XCD block (wg_coords)
+  int tt, vt, splits;      // token tiles, vocab tiles, vocab splits
+  int xa, xb;              // XCD round block (wg_coords), 0 = unblocked
   RowPart* part;           // [N][splits] (max, sum-exp) of the stored bf16 values, or null
 };
 
@@ -138,7 +139,7 @@ void fp8_head_kernel(Fp8Params p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_t* lds = (lds_t*)lds_raw;
   int tile_t, split;
-  wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, tile_t, split);
+  wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, p.xb, tile_t, split);
   const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
   const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
   const int tid = threadIdx.x;
@@ -377,7 +378,7 @@ void fp8_head_kernel(Fp8Params p) {
 }
 
 struct Fp8Plan {
-  int tt, vt, splits, xa;
+  int tt, vt, splits, xa, xb;
 };
 
 Fp8Plan fp8_plan(int64_t n, int64_t v) {
@@ -387,13 +388,13 @@ Fp8Plan fp8_plan(int64_t n, int64_t v) {
   int cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  int sp = pl.tt > 0 ? (cus + pl.tt - 1) / pl.tt : 1;   // no rows: nothing launches
-  sp = sp < 1 ? 1 : (sp > pl.vt ? pl.vt : sp);
-  pl.splits = sp;
   // one stage reads FN x 128 activation codes per token tile and FM x 128 weight codes per
-  // split: at N = 4096 this picks 8 token tiles x 4 splits per XCD, 20% fewer L2 fills
-  // than 4 x 8 and 1.2% faster
-  pl.xa = xcd_block(pl.tt, sp, FN, FM);
+  // split: at N = 4096 this picks 8 splits in blocks of 8 token tiles x 4 splits per XCD,
+  // 20% fewer L2 fills than 4 x 8 and 1.2% faster
+  const SplitPlan sp = split_plan(pl.tt, pl.vt, cus, FN, FM);
+  pl.splits = sp.splits;
+  pl.xa = sp.xa;
+  pl.xb = sp.xb;
   return pl;
 }
 
@@ -431,7 +432,7 @@ hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int
   p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
   p.n = n; p.v = v; p.d = d;
   const Fp8Plan pl = fp8_plan(n, v);
-  p.vt = pl.vt; p.tt = pl.tt; p.splits = pl.splits; p.xa = pl.xa;
+  p.vt = pl.vt; p.tt = pl.tt; p.splits = pl.splits; p.xa = pl.xa; p.xb = pl.xb;
   const int sp = pl.splits;
   p.part = lse ? part : nullptr;
   static bool attr_set = false;

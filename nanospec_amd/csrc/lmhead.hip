@@ -530,7 +530,7 @@ struct HeadParams {
   int64_t ldh, ldw, ldm, ldt;
   int64_t n, d, v;
   int tt, vt, splits;       // token tiles, vocab tiles, vocab splits
-  int xa;                   // token tiles per XCD block (wg_coords), 0 = unblocked
+  int xa, xb;               // XCD round block (wg_coords), 0 = unblocked
   // Markov head as a second K segment (r > 0): z += W1[prev] . W2^T
   const int64_t* prev;      // [N] previous-token ids
   const uint16_t* w1;       // [V, r] bf16 (embedding)
@@ -845,7 +845,7 @@ void head_kernel(HeadParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_t* lds = (lds_t*)lds_raw;
   int tile_t, split;
-  wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, tile_t, split);
+  wg_coords(blockIdx.x, gridDim.x, p.tt, p.xa, p.xb, tile_t, split);
   const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
   const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
   const int tid = threadIdx.x;
@@ -1093,7 +1093,7 @@ int device_cus() {
 
 struct HeadPlan {
   int tt, vt, splits, grid;
-  int xa;  // token tiles per XCD block, 0 = unblocked (wg_coords)
+  int xa, xb;  // XCD round block (wg_coords): token tiles x splits, 0 = unblocked
 };
 
 
@@ -1101,13 +1101,12 @@ HeadPlan head_plan(int64_t n, int64_t v) {
   HeadPlan pl;
   pl.tt = (int)((n + BN - 1) / BN);
   pl.vt = (int)((v + BM - 1) / BM);
-  const int cus = device_cus();
-  int s = pl.tt > 0 ? (cus + pl.tt - 1) / pl.tt : 1;   // no rows: nothing launches
-  if (s < 1) s = 1;
-  if (s > pl.vt) s = pl.vt;
-  pl.splits = s;
-  pl.grid = pl.tt * s;
-  pl.xa = xcd_block(pl.tt, s);
+  // both operands stage 256 rows x 64 bf16 per K step, so the block only counts tiles
+  const SplitPlan sp = split_plan(pl.tt, pl.vt, device_cus());
+  pl.splits = sp.splits;
+  pl.grid = pl.tt * sp.splits;
+  pl.xa = sp.xa;
+  pl.xb = sp.xb;
   return pl;
 }
 
@@ -1228,7 +1227,7 @@ HeadParams head_params(const void* hidden, int64_t ldh, const void* weight, int6
   p.teacher = teacher;
   p.ldh = ldh; p.ldw = ldw; p.ldm = ldm; p.ldt = ldt;
   p.n = a.n; p.d = d; p.v = v;
-  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa;
+  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa; p.xb = pl.xb;
   p.labels = a.labels; p.weights = a.weights;
   p.c_ce = a.c_ce; p.c_kl = a.c_kl; p.inv_acc = a.inv_acc;
   p.part1 = w.part1; p.zy = w.zy; p.parta = w.parta; p.partk = w.partk;
@@ -1368,7 +1367,7 @@ hipError_t lmhead_linear_lse(const void* x, int64_t ldx, const int64_t* rows, in
   p.markov = static_cast<const uint16_t*>(addend);
   p.ldh = ldx; p.ldw = ldw; p.ldm = lda;
   p.n = n; p.d = d; p.v = v;
-  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa;
+  p.tt = pl.tt; p.vt = pl.vt; p.splits = pl.splits; p.xa = pl.xa; p.xb = pl.xb;
   p.out = static_cast<uint16_t*>(out); p.ldo = ldo;
   p.teacher = nullptr;
   p.hrows = rows; p.nh = nrows;

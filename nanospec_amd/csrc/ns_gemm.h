@@ -142,19 +142,22 @@ __device__ __forceinline__ void fill_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Workgroup -> (tile t, split s) map for a persistent grid of TT x S workgroups.
-// Workgroups are dispatched round-robin over the 8 XCDs, and the C = G / 8 workgroups of
-// one XCD share its L2.  With xa > 0 each XCD holds a block of xa t-tiles x (C / xa)
-// splits, so one K stage of the block reads xa + C / xa distinct operand tiles through
-// that L2 (12 for a 4 x 8 block, against 18 for 16 x 2).  xa = 0: consecutive ids per
-// XCD, t fastest.
-__device__ __forceinline__ void wg_coords(int g, int G, int TT, int xa, int& t, int& s) {
+// Workgroup -> (tile t, split s) map for a grid of TT x S workgroups, one per CU at a
+// time.  Workgroups are dispatched round-robin over the 8 XCDs, and the workgroups of
+// one XCD share its L2.  With xa > 0 the grid runs in rounds of xa * xb workgroups per
+// XCD (one per CU), and each round of an XCD is a block of xa t-tiles x xb splits, so one
+// K stage of the round reads xa + xb distinct operand tiles through that L2 (12 for a
+// 4 x 8 block, against 18 for 16 x 2).  Block b = round * 8 + XCD walks the
+// (TT / xa) x (S / xb) block grid, t-blocks fastest.  Requires G % (8 xa xb) == 0,
+// TT % xa == 0 and S % xb == 0 (split_plan).  xa = 0: consecutive ids per XCD, t fastest.
+__host__ __device__ inline void wg_coords(int g, int G, int TT, int xa, int xb, int& t, int& s) {
   if (xa > 0) {
-    const int C = G / kNumXcd, xb = C / xa;
-    const int x = g % kNumXcd, r = g / kNumXcd;
-    const int groups_t = TT / xa;
-    t = (x % groups_t) * xa + r % xa;
-    s = (x / groups_t) * xb + r / xa;
+    const int C = xa * xb;
+    const int x = g % kNumXcd, i = g / kNumXcd;
+    const int blk = (i / C) * kNumXcd + x, r = i % C;
+    const int gm = TT / xa;
+    t = (blk % gm) * xa + r % xa;
+    s = (blk / gm) * xb + r / xa;
     return;
   }
   int L = g;
@@ -163,19 +166,40 @@ __device__ __forceinline__ void wg_coords(int g, int G, int TT, int xa, int& t, 
   t = L % TT;
 }
 
-// t-tiles per XCD block for a tt x splits grid (wg_coords): a divisor a of C = grid / 8
-// with tt % a == 0 and splits % (C / a) == 0, minimising the distinct operand bytes one
-// L2 serves per K stage, a * t_stage + (C / a) * s_stage (t_stage: one t-tile's operand
-// stage, shared by the block's splits; s_stage: one split's); ties keep the smaller a.
-// 0 when no such block exists.
-inline int xcd_block(int tt, int splits, int64_t t_stage = 1, int64_t s_stage = 1) {
-  const int grid = tt * splits;
-  if (grid % kNumXcd) return 0;
-  const int C = grid / kNumXcd;
-  int best = 0;
-  for (int a = 1; a <= C; ++a) {
-    if (C % a || tt % a || splits % (C / a)) continue;
-    if (best == 0 || a * t_stage + (C / a) * s_stage < best * t_stage + (C / best) * s_stage) best = a;
+struct SplitPlan {
+  int splits;   // S: vocab (or column) ranges, one workgroup each per t-tile
+  int xa, xb;   // round block for wg_coords, 0 = unblocked
+};
+
+// Splits and XCD block for a TT-tile grid over `vt` splittable tiles (vocab tiles) on
+// `cus` CUs, one workgroup per CU at a time.  Candidates are the split counts S up to
+// max(64, cus / TT) (and at most vt) whose grid TT * S fills whole rounds of cus
+// workgroups.  Each gets the block a x b = cus / 8 with a | TT and b | S minimising the
+// distinct operand bytes one L2 serves per K stage, a * t_stage + b * s_stage (t_stage:
+// one t-tile's operand stage, shared by the block's splits; s_stage: one split's).  The
+// cheapest wins, ties keeping fewer splits, then the smaller a.  Without a candidate:
+// floor(cus / TT) splits (at least 1), unblocked, so no round is left with a few
+// stragglers.
+inline SplitPlan split_plan(int tt, int vt, int cus, int64_t t_stage = 1, int64_t s_stage = 1) {
+  int s0 = tt > 0 && tt <= cus ? cus / tt : 1;   // no tiles: nothing launches
+  if (s0 > vt) s0 = vt;
+  if (s0 < 1) s0 = 1;
+  SplitPlan best = {s0, 0, 0};
+  if (tt <= 0 || cus <= 0 || cus % kNumXcd) return best;
+  const int C = cus / kNumXcd;
+  int64_t best_cost = -1;
+  int s_max = cus / tt > 64 ? cus / tt : 64;
+  if (s_max > vt) s_max = vt;
+  for (int sp = 1; sp <= s_max; ++sp) {
+    if (((int64_t)tt * sp) % cus) continue;
+    for (int a = 1; a <= C; ++a) {
+      if (C % a || tt % a || sp % (C / a)) continue;
+      const int64_t cost = a * t_stage + (C / a) * s_stage;
+      if (best_cost < 0 || cost < best_cost) {
+        best_cost = cost;
+        best = {sp, a, C / a};
+      }
+    }
   }
   return best;
 }

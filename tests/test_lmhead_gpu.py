@@ -105,6 +105,7 @@ def test_c0_full_oracle(gpu_lib):
     (72, 128, 8200),     # partial token tile, partial vocab tile, V % 64 != 0 (dh K tail)
     (264, 192, 2056),    # two token tiles, one vocab tile plus a sliver
     (512, 64, 16384),    # several vocab splits
+    (3072, 128, 16384),  # 12 token tiles: 64 splits in three rounds of 4 x 8 XCD blocks
 ])
 def test_odd_shapes(gpu_lib, n, d, v):
     hidden, weight, markov, teacher, slots = synthetic.head_inputs(n, d, v, 77 + n, DEV)
