@@ -33,6 +33,9 @@
  *   - dtype codes: NS_BF16 (raw bfloat16) or NS_F32.
  *   - Row metadata: labels int64 [N], weights fp32 [N] (valid * exp(-slot/gamma)),
  *     valid uint8 [N] (torch.bool); rows come in blocks of K consecutive slots.
+ *     Label -100 is F.cross_entropy's ignore_index (objective.py:54): the row has no CE
+ *     term (CE 0, and dl without it).  Any other label outside [0, V) makes the row's CE,
+ *     and so the loss, NaN: the device cannot raise.
  *   - Outputs: metrics fp32 [6] in LossMetrics order (ce, kl, numerator,
  *     denominator, accept_len_sum, accept_len_total; objective.py:11-18) and
  *     row_stats fp32 [N][8] = (lse_z, lse_u, ce, kl, accept_rate, z_label, 0, 0).

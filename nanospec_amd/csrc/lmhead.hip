@@ -896,7 +896,8 @@ void head_kernel(HeadParams p) {
       const float w = p.weights[trow] * p.inv_acc;
       cr[0] = p.row_stats[trow * kRowStatWidth + kLseZ] * kLog2e;
       cr[1] = p.row_stats[trow * kRowStatWidth + kLseU] * kLog2e;
-      cr[2] = w * (p.c_ce + p.c_kl);
+      // an ignored row has no CE term: dl = w c_kl (p - t) (its label matches no entry)
+      cr[2] = p.labels[trow] == kIgnoreIndex ? w * p.c_kl : w * (p.c_ce + p.c_kl);
       cr[3] = w * p.c_kl;
       cr[4] = w * p.c_ce;
     }

@@ -218,6 +218,10 @@ struct alignas(32) RowPart {
   float mz, sz, mu, su, A, pad0, pad1, pad2;
 };
 
+// F.cross_entropy's default ignore_index (objective.py:54): a row with this label has no
+// CE term (CE 0) and no CE gradient.  Any other label outside [0, V) makes CE NaN.
+constexpr int64_t kIgnoreIndex = -100;
+
 // Per-row statistics returned to the host (layout of row_stats[N][8]).
 enum RowStat : int {
   kLseZ = 0, kLseU = 1, kCE = 2, kKL = 3, kAccept = 4, kZy = 5, kRowStatWidth = 8

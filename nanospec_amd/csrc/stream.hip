@@ -174,13 +174,14 @@ __global__ __launch_bounds__(256) void merge_kernel(const RowPart* __restrict__ 
     const int64_t tr = ts.rows ? ts.rows[r] : r;
     lu = (tr >= 0 && tr < ts.nt) ? ts.lse[tr] : __builtin_nanf("");
   }
-  // A label outside [0, V) has no logit: CE becomes NaN (the loss reports it, never masks it).
+  // A label outside [0, V) has no logit: CE becomes NaN (the loss reports it, never masks
+  // it), except kIgnoreIndex, whose CE is 0 (lz - lz keeps a poisoned row's NaN).
   const int64_t label = labels[r];
   const float y = (label >= 0 && label < v) ? zy[r] : __builtin_nanf("");
   float* o = row_stats + r * kRowStatWidth;
   o[kLseZ] = lz;
   o[kLseU] = lu;
-  o[kCE] = lz - y;
+  o[kCE] = label == kIgnoreIndex ? lz - lz : lz - y;
   o[kKL] = ts.lse ? 0.f : st.A / st.su - lu + lz;
   o[kZy] = y;
   o[6] = 0.f;   // reserved columns of the row_stats layout
@@ -234,8 +235,9 @@ __global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
   const float lzl = row_stats[r * kRowStatWidth + kLseZ] * kLog2e;
   const float lul = row_stats[r * kRowStatWidth + kLseU] * kLog2e;
   const float w = weights[r] * inv_acc;
-  const float cp = w * (c_ce + c_kl), ct = w * c_kl, cy = w * c_ce;
   const int64_t y = labels[r];
+  // an ignored row has no CE term: dl = w c_kl (p - t) (its label matches no entry)
+  const float cp = y == kIgnoreIndex ? w * c_kl : w * (c_ce + c_kl), ct = w * c_kl, cy = w * c_ce;
   float acc = 0.f;
   int64_t scalar_from = lo;
   if (VEC && lo < hi) {

@@ -96,6 +96,8 @@ def ce_kl_loss(logits, target_logits, prepared, objective, *, accumulation_steps
     ``logits`` / ``target_logits``: [..., K, V] bf16 or fp32 on one device.
     ``prepared``: any object with ``weights`` (fp32), ``target_ids`` (int64) and
     ``valid`` (bool), each [..., K] -- e.g. the reference's PreparedBatch.
+    A target id of -100 is F.cross_entropy's ignore_index: that row has no CE term.  Any
+    other id outside [0, V) makes the loss NaN (the reference raises; the device cannot).
     Keyword extensions: ``accumulation_steps`` pre-scales the dl emitted with the
     forward; ``emit_dlogits=False`` skips it (metrics only).
     """

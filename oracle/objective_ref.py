@@ -190,16 +190,30 @@ def _lse(x: np.ndarray) -> np.ndarray:
     return (m + np.log(np.exp(x - m).sum(-1, keepdims=True)))[..., 0]
 
 
+# F.cross_entropy's default ignore_index (objective.py:54): such a row has no CE term.
+IGNORE_INDEX = -100
+
+
+def _checked_labels(labels, v):
+    """labels as int64 and the mask of ignored rows; any other label outside [0, V)
+    raises, as F.cross_entropy does."""
+    labels = np.asarray(labels, dtype=np.int64)
+    ignore = labels == IGNORE_INDEX
+    if np.any(((labels < 0) | (labels >= v)) & ~ignore):
+        raise ValueError(f"label outside [0, {v}) other than the ignore index {IGNORE_INDEX}")
+    return labels, ignore
+
+
 def row_objective(z, u, labels, dtype=np.float64) -> dict:
     """Per-row CE, KL(target || draft) and acceptance rate a = sum_v min(p, t).
 
-    z, u: [R, V] draft / teacher logits; labels [R].  Computed in ``dtype``
-    (float64 for parity, float32 for the CPU baseline).  Follows
+    z, u: [R, V] draft / teacher logits; labels [R] (IGNORE_INDEX: CE 0).  Computed in
+    ``dtype`` (float64 for parity, float32 for the CPU baseline).  Follows
     objective.py:54 (CE), 55-58 (softmax, log_softmax, KL) and 42 (accept rate).
     """
     z = np.asarray(z, dtype=dtype)
     u = np.asarray(u, dtype=dtype)
-    labels = np.asarray(labels, dtype=np.int64)
+    labels, ignore = _checked_labels(labels, z.shape[1])
     r = np.arange(z.shape[0])
     lz, lu = _lse(z), _lse(u)
     logp = z - lz[:, None]
@@ -208,7 +222,7 @@ def row_objective(z, u, labels, dtype=np.float64) -> dict:
     return dict(
         lse_z=lz,
         lse_u=lu,
-        ce=lz - z[r, labels],
+        ce=np.where(ignore, 0.0, lz - z[r, np.where(ignore, 0, labels)]).astype(lz.dtype),
         kl=(t * (logt - logp)).sum(-1),
         accept_rate=np.minimum(p, t).sum(-1),
     )
@@ -273,16 +287,20 @@ def ce_kl_backward(z, u, weights, labels, c_ce=0.1, c_kl=0.9, accumulation_steps
     """dl = (w / acc) [c_ce (p - e_y) + c_kl (p - t)]  (objective.py:70-80).
 
     The derivative of the *numerator* (not divided by the denominator); the
-    pooled normalisation happens in the optimizer (shard.py:318-331).
+    pooled normalisation happens in the optimizer (shard.py:318-331).  A row labelled
+    IGNORE_INDEX has no CE term, so its dl is (w / acc) c_kl (p - t): the gradient of the
+    forward's loss (the reference's scatter_add_ at objective.py:78 rejects that index).
     """
     z = np.asarray(z, dtype=dtype)
     u = np.asarray(u, dtype=dtype)
     n = z.shape[0]
+    labels, ignore = _checked_labels(np.asarray(labels).reshape(n), z.shape[1])
     scale = np.asarray(weights, dtype=dtype).reshape(n) / accumulation_steps
     p = np.exp(z - _lse(z)[:, None])
     t = np.exp(u - _lse(u)[:, None])
-    dl = (c_ce + c_kl) * p - c_kl * t
-    dl[np.arange(n), np.asarray(labels).reshape(n)] -= c_ce
+    dl = np.where(ignore[:, None], c_kl * (p - t), (c_ce + c_kl) * p - c_kl * t)
+    keep = np.flatnonzero(~ignore)
+    dl[keep, labels[keep]] -= c_ce
     return dl * scale[:, None]
 
 

@@ -86,6 +86,34 @@ def test_reemitted_dl_matches_oracle(gpu_lib):
     assert masked.any() and np.all(got[masked] == 0.0)      # w = 0 rows vanish
 
 
+def test_ignore_index_rows(gpu_lib):
+    """Label -100 in the fused head: CE 0 and dl without the CE term, against the oracle,
+    in the forward's emission and in the backward's re-emission."""
+    hidden, weight, target, slots, kw, markov = _case("dense")
+    y = slots.target_ids.clone()
+    y.view(-1)[[0, 7, 64, 135]] = -100
+    slots = synthetic.Slots(slots.weights, y, slots.valid)
+    o = Objective(block_size=8)
+    m, saved = head.lm_head_ce_kl_loss(hidden, weight, target, slots, o, accumulation_steps=2, **kw)
+    dl2 = saved.dlogits.clone()
+    head.lm_head_ce_kl_backward(saved, 2)                                   # hands the emitted dl over
+    _, dl2_again = head.lm_head_ce_kl_backward(saved, 2, return_dlogits=True)   # pass 2 again
+    torch.cuda.synchronize()
+    assert torch.equal(dl2_again.reshape(dl2.shape), dl2)
+    assert np.all(_np(saved.row_stats)[[0, 7, 64, 135], 2] == 0.0)
+    z = ref.lm_head_logits(_np(hidden), _np(weight), _np(markov))
+    wt = _np(slots.weights).reshape(-1)
+    yy = y.reshape(-1).cpu().numpy()
+    m_ref, _ = ref.ce_kl_loss(z, _np(target), wt.reshape(-1, 8), yy.reshape(-1, 8), slots.valid.cpu().numpy(),
+                              o.ce, o.kl)
+    for f in ("ce", "kl", "numerator", "accept_len_sum"):
+        assert float(getattr(m, f)) == pytest.approx(m_ref[f], rel=1e-4, abs=1e-6), f
+    want = ref.ce_kl_backward(z, _np(target), wt, yy, o.ce, o.kl, accumulation_steps=2)
+    got = _np(dl2).reshape(want.shape).astype(np.float64)
+    tol = np.abs(want) * 2.0 ** -7 + 2e-5 * np.abs(want).max(axis=-1, keepdims=True)
+    assert np.all(np.abs(got - want) <= tol)
+
+
 def test_empty_batch(gpu_lib):
     d, v = 128, 4096
     hidden = torch.empty((0, 8, d), dtype=torch.bfloat16, device=DEV)

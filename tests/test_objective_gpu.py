@@ -158,6 +158,25 @@ def test_empty_supervision(gpu_lib):
     assert torch.count_nonzero(dl) == 0
 
 
+def test_ignore_index_and_out_of_range_labels(gpu_lib):
+    """Label -100 (F.cross_entropy's ignore_index, objective.py:54): CE 0 and no CE term in
+    dl, as the oracle (pinned to torch's cross_entropy and autograd); any other label
+    outside [0, V) makes the loss NaN instead of raising on the device."""
+    z, u, slots = synthetic.logits_inputs(32, 3000, 15, DEV)
+    y = slots.target_ids.clone()
+    y.view(-1)[[2, 9, 17]] = -100
+    slots = synthetic.Slots(slots.weights, y, slots.valid)
+    o = Objective(block_size=8)
+    m, saved, dl = _run(z, u, slots, o, acc=2)
+    m_ref, rows, dl_ref = _oracle(z, u, slots, o, acc=2)
+    _assert_metrics(_metrics(m), m_ref)
+    assert np.all(_np(saved.row_stats)[[2, 9, 17], 2] == 0.0)
+    _assert_dl_bf16(_np(dl).reshape(32, -1), dl_ref)
+    y.view(-1)[4] = 3000
+    m, _, _ = _run(z, u, synthetic.Slots(slots.weights, y, slots.valid), o)
+    assert np.isnan(float(m.loss))
+
+
 def test_nan_propagates(gpu_lib):
     z, u, slots = synthetic.logits_inputs(16, 2048, 14, DEV)
     z[3, 100] = float("nan")

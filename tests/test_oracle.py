@@ -160,6 +160,30 @@ def test_loss_and_dl_match_torch_library_and_autograd():
     np.testing.assert_allclose(dl, grad, rtol=1e-9, atol=1e-15)
 
 
+def test_ignore_index_matches_torch_cross_entropy_and_autograd():
+    """Label -100 is F.cross_entropy's default ignore_index (objective.py:54): CE 0 in the
+    forward, and dl is the gradient of that loss (no CE term on the row)."""
+    n, v, k = 16, 211, 8
+    z, u = _logits(20, n, v), _logits(21, n, v, scale=3.0, peak=8.0)
+    y = np.random.default_rng(22).integers(0, v, n)
+    y[[1, 6, 9]] = ref.IGNORE_INDEX
+    valid = np.ones((n // k, k), dtype=bool)
+    w = ref.slot_weights(valid, 4.0).reshape(-1)
+    rows = ref.row_objective(z, u, y)
+    lib = F.cross_entropy(torch.from_numpy(z), torch.from_numpy(y), reduction="none").numpy()
+    np.testing.assert_allclose(rows["ce"], lib, rtol=1e-12, atol=1e-12)
+    assert np.all(rows["ce"][[1, 6, 9]] == 0.0)
+    m, _ = ref.ce_kl_loss(z, u, w.reshape(-1, k), y.reshape(-1, k), valid, 0.1, 0.9)
+    num, _, _, grad = _library_loss(z, u, w, y, 0.1, 0.9, acc=2)
+    assert m["numerator"] == pytest.approx(num, rel=1e-12)
+    dl = ref.ce_kl_backward(z, u, w, y, 0.1, 0.9, accumulation_steps=2)
+    np.testing.assert_allclose(dl, grad, rtol=1e-9, atol=1e-15)
+    with pytest.raises(ValueError):
+        ref.row_objective(z, u, np.full(n, -1))
+    with pytest.raises(ValueError):
+        ref.ce_kl_backward(z, u, w, np.full(n, v), 0.1, 0.9)
+
+
 def test_dl_invariants():
     n, v = 16, 129
     z, u = _logits(11, n, v), _logits(12, n, v)
