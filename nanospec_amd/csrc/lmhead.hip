@@ -261,10 +261,13 @@ __device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la
 // between them:
 //   step 0: fragment reads for step 1 | B fills of stage t + 1
 //   steps 1, 2: fragment reads for the next step
-//   step 3: after four groups, fill_barrier (stage t + 1 complete, buffer t & 1 read by
-//           everyone), then fragment reads of stage t + 1 step 0 and the A fills of
-//           stage t + 2 into buffer t & 1.
-// Fills past the last stage re-read the last stage into the idle buffer.
+//   step 3: fill_barrier first (stage t + 1 complete; every wave's reads of buffer t & 1,
+//           the last issued in step 2, done), then in its first eight slots the fragment
+//           reads of stage t + 1 step 0 and the A fills of stage t + 2 into buffer t & 1.
+// The barrier cannot come earlier: step 2 still reads buffer t & 1 and the step-0
+// fragment registers.  Placing it at the start of step 3 rather than after two of its
+// MFMA groups gives the next stage's first reads 8 more slots: 3.6-3.9% off each head
+// pass at C2.  Fills past the last stage re-read the last stage into the idle buffer.
 //
 // The operand tiles come in ready-made: `ta`/`tb` hold the per-lane offsets of the
 // 256 rows of each operand from the uniform bases `pa`/`pb` (stage 0), and stage t reads
@@ -297,6 +300,7 @@ __device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTi
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int cb = kk & 1;
+      if (kk == 3) fill_barrier();
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
@@ -313,18 +317,17 @@ __device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTi
                   cur + kStageBytes + lds_off(wn * 128 + i * 32 + r, (kk + 1) * 2 + kh));
           }
           if (kk == 0 && q >= 2) tb.issue(pb + k1, nxt + kStageBytes, wv, (q - 2) * 4 + j);
-          if (kk == 3 && q >= 2) {
+          if (kk == 3 && q < 2) {
             if ((j & 1) == 0)
               f[0].a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
                   nxt + lds_off(wm * 128 + i * 32 + r, kh));
             else
               f[0].b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
                   nxt + kStageBytes + lds_off(wn * 128 + i * 32 + r, kh));
-            ta.issue(pa + k2, buf(t), wv, (q - 2) * 4 + j);
+            ta.issue(pa + k2, buf(t), wv, q * 4 + j);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (kk == 3 && q == 1) fill_barrier();
       }
     }
   }
@@ -349,8 +352,8 @@ __device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
 // without registers, as in gemm_nt; B fragments use transposed LDS reads.  Per stage t:
 //   steps 0-2: the next step's 12 fragment reads (4 A, 8 B halves), one per MFMA;
 //   step 0: the B fills of stage t + 1 in the first eight MFMA slots;
-//   step 3: fill_barrier after two groups, then stage t + 1's step-0 fragments and the
-//           A fills of stage t + 2.
+//   step 3: fill_barrier first (as in gemm_nt_tiles), then in its first eight slots stage
+//           t + 1's step-0 fragments and the A fills of stage t + 2.
 // Ends with a barrier.  KT >= 1.
 __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
                                             int64_t a0, int64_t amax, const uint16_t* __restrict__ B,
@@ -404,6 +407,7 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int cb = kk & 1;
+      if (kk == 3) fill_barrier();
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
@@ -413,8 +417,8 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
           __builtin_amdgcn_sched_barrier(0);
           if (kk < 3 && sl < 12) read_op(cb ^ 1, cur, kk + 1, sl);
           if (kk == 0 && sl < 8) tb.issue(pb + t1 * ldb_stage, nxt + kStageBytes, wv, sl);
-          if (kk == 3 && sl >= 8) {
-            const int u = sl - 8;
+          if (kk == 3 && sl < 8) {
+            const int u = sl;
             if (u < 4) {
               read_op(0, nxt, 0, 2 * u);
               read_op(0, nxt, 0, 2 * u + 1);
@@ -425,7 +429,6 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
           }
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (kk == 3 && q == 1) fill_barrier();
       }
     }
   }
