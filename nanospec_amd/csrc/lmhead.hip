@@ -817,7 +817,7 @@ __device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, i
         for (int e = 0; e < 8; ++e) {
           const float pp = fast_exp2(__builtin_fmaf(z[8 * k + e], kLog2e, -lzl));
           const float tt = fast_exp2(__builtin_fmaf(u[8 * k + e], kLog2e, -lul));
-          aloc += fminf(pp, tt);
+          aloc += min_nonneg(pp, tt);
           // KL's sum t (u - z) (entries past V: t = 0 and u = z)
           if (FLAGS & kTeacherLse) kloc = __builtin_fmaf(tt, u[8 * k + e] - z[8 * k + e], kloc);
           d[e] = __builtin_fmaf(cp, pp, -ct * tt);

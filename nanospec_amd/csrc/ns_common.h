@@ -33,6 +33,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
 // exp(x) as 2^(x*log2e) with the hardware exp2; callers fold the scale into an FMA.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// fminf(a, b) for a, b >= +0 or NaN (probabilities): on such values the unsigned order of
+// the bit patterns is the float order, and a NaN pattern is above every number, so the
+// integer min returns what fminf returns (the number when one side is NaN).  One v_min_u32,
+// where fminf costs a v_max_f32 per operand (canonicalising the exp2 results) plus v_min_f32.
+__device__ __forceinline__ float min_nonneg(float a, float b) {
+  const uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+  return __uint_as_float(x < y ? x : y);
+}
+
 // ---- 8-element vector loads / stores (16 B for bf16, 32 B for f32) -----------
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {

@@ -266,7 +266,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
         for (int e = 0; e < 8; ++e) {
           const float p = fast_exp2(__builtin_fmaf(zf[q][e], kLog2e, -lzl));
           const float t = fast_exp2(__builtin_fmaf(uf[q][e], kLog2e, -lul));
-          if (ACCEPT) acc += fminf(p, t);
+          if (ACCEPT) acc += min_nonneg(p, t);
           if (EMIT) d[e] = __builtin_fmaf(cp, p, -ct * t);
         }
         if (EMIT) {
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
   for (int64_t i = scalar_from + threadIdx.x; i < hi; i += kStreamThreads) {
     const float p = fast_exp2(__builtin_fmaf(load1(zr + i), kLog2e, -lzl));
     const float t = fast_exp2(__builtin_fmaf(load1(ur + i), kLog2e, -lul));
-    if (ACCEPT) acc += fminf(p, t);
+    if (ACCEPT) acc += min_nonneg(p, t);
     if (EMIT) {
       float d = __builtin_fmaf(cp, p, -ct * t);
       if (i == y) d -= cy;
