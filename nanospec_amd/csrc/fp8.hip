@@ -435,13 +435,9 @@ hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int
   p.vt = pl.vt; p.tt = pl.tt; p.splits = pl.splits; p.xa = pl.xa; p.xb = pl.xb;
   const int sp = pl.splits;
   p.part = lse ? part : nullptr;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_head_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kFp8Lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr_done{0};
+  if (const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&fp8_head_kernel), kFp8Lds, attr_done))
+    return e;
   {
     NS_TIMED("fp8_head_gemm", st);
     hipLaunchKernelGGL(fp8_head_kernel, dim3((unsigned)(p.tt * sp)), dim3(kThreads), kFp8Lds, st, p);

@@ -1084,14 +1084,19 @@ __global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict_
   *reinterpret_cast<uint2*>(dh + row * lddh + col) = o;
 }
 
+// CUs of the current device (cached per device id below 64; 256 when the query fails, as
+// on a host without a GPU, where only workspace sizes are asked for)
 int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
   }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev >= 0 && dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
@@ -1185,13 +1190,10 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
 
 template <int MODE, typename TT, int FLAGS = 0>
 hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char* name) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHeadLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr_done{0};
+  if (const hipError_t e =
+          ensure_dynamic_lds(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>), kHeadLdsBytes, attr_done))
+    return e;
   NS_TIMED(name, st);
   hipLaunchKernelGGL((head_kernel<MODE, TT, FLAGS>), dim3(grid), dim3(kThreads), kHeadLdsBytes, st, p);
   return hipGetLastError();
@@ -1316,13 +1318,9 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
   const size_t b_part2 = align_up((size_t)pl.ksplit2 * n * r * sizeof(float), 256);
   p.part2 = reinterpret_cast<float*>(static_cast<char*>(ws) + b_part);
   void* norm_ws = static_cast<char*>(ws) + b_part + b_part2;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dh_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr_done{0};
+  if (const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&dh_kernel), kLdsBytes, attr_done))
+    return e;
   {
     NS_TIMED("dh_gemm", st);
     hipLaunchKernelGGL(dh_kernel, dim3(pl.grid), dim3(kThreads), kLdsBytes, st, p);

@@ -286,13 +286,8 @@ hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int6
     p.w2g = static_cast<uint16_t*>(w2_grad); p.ldg2 = ldg2;
     p.n = n; p.v = v; p.r = r;
     p.ct = (int)((r + TN - 1) / TN);
-    static bool attr_set = false;
-    if (!attr_set) {
-      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dw2_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   kLds)) != hipSuccess)
-        return e;
-      attr_set = true;
-    }
+    static std::atomic<uint64_t> attr_done{0};
+    if ((e = ensure_dynamic_lds(reinterpret_cast<const void*>(&dw2_kernel), kLds, attr_done)) != hipSuccess) return e;
     NS_TIMED("markov_dw2", st);
     const int grid = (int)((v + TM - 1) / TM) * p.ct;
     hipLaunchKernelGGL(dw2_kernel, dim3(grid), dim3(kThreads), kLds, st, p);

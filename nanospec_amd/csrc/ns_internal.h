@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "ns_common.h"
 
 namespace ns {
@@ -145,5 +147,19 @@ hipError_t pooled_tail(const float* metrics, int64_t count, int64_t world_size, 
 hipError_t scale_gradient(void* grad, int dtype, int64_t n, const float* factor, hipStream_t st);
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device.  The attribute
+// belongs to each device's copy of the kernel, so `done` keeps one bit per device id (ids
+// of 64 and up set it on every call); concurrent first calls may both set it, harmlessly.
+inline hipError_t ensure_dynamic_lds(const void* fn, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t(1) << dev) : 0;
+  if (bit && (done.load(std::memory_order_relaxed) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_relaxed);
+  return e;
+}
 
 }  // namespace ns
