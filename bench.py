@@ -6,7 +6,7 @@ and dhidden when the LM head is fused), with the dominant kernel's roofline
 fraction.  A "step" is one pass of the hot path over one batch of synthetic
 input that is already resident in HBM.
 
-    python bench.py [--steps K] [--warmup W] [--config c1|c2|c3|c4]
+    python bench.py [--steps K] [--warmup W] [--config c1|c2|c2x|c3|c4]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a
 message (the path is data-parallel over slots; the library has no collectives).
