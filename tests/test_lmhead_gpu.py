@@ -175,6 +175,40 @@ def _check_large(hidden, weight, markov, teacher, slots, o, blocks):
     np.testing.assert_allclose(rs[rows, 4], r["accept_rate"], atol=2e-5)
     _assert_dl(_np(dl.reshape(-1, dl.shape[-1])[rows]), dl_ref)
     _assert_dh(_np(dh.reshape(-1, dh.shape[-1])[rows]), dh_ref)
+    _assert_row_properties(rs, dl, dh, weight, slots)
+
+
+def _assert_row_properties(rs, dl, dh, weight, slots):
+    """Size-independent properties on every row of a full-size run:
+    * CE = lse_z - z_y >= 0, KL >= 0 and 0 <= accept rate <= 1;
+    * each dl row sums to ~0 (sum p = sum t = 1 cancels the three terms) and masked rows
+      are exactly 0;
+    * dh = dl . W on every row, through a random projection r: dh r = dl (W r), to the
+      bf16 rounding of dh (2^-8 of sum |dh_j r_j|) plus 1e-5 of the largest such sum."""
+    assert np.all(rs[:, 2] >= -1e-4) and np.all(rs[:, 3] >= -1e-4)
+    assert np.all((rs[:, 4] >= 0.0) & (rs[:, 4] <= 1.0 + 1e-5))
+    d = weight.shape[1]
+    dl2, dh2 = dl.reshape(-1, dl.shape[-1]), dh.reshape(-1, d)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    r = torch.randn(d, generator=g, device=DEV)
+    wr = weight.float() @ r
+    masked = ~slots.valid.reshape(-1)
+    lhs, rhs, mag = [], [], []
+    for i in range(0, dl2.shape[0], 4096):     # fp32 copies a chunk of rows at a time
+        dlf = dl2[i:i + 4096].float()
+        row_sum = dlf.sum(-1).abs()
+        row_abs = dlf.abs().sum(-1).clamp_min(1e-30)
+        assert float((row_sum / row_abs).max()) < 1e-2, i
+        assert torch.count_nonzero(dl2[i:i + 4096][masked[i:i + 4096]]) == 0, i
+        dhf = dh2[i:i + 4096].float()
+        lhs.append(dhf @ r)
+        rhs.append(dlf @ wr)
+        mag.append(dhf.abs() @ r.abs())
+        del dlf, dhf
+    lhs, rhs, mag = torch.cat(lhs), torch.cat(rhs), torch.cat(mag)
+    err = (lhs - rhs).abs()
+    tol = 2.0 ** -8 * mag + 1e-5 * mag.max()
+    assert bool((err <= tol).all()), float((err - tol).max())
 
 
 def test_c2_full_size(gpu_lib):
