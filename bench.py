@@ -535,8 +535,9 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the "
-              "objective path is data-parallel over slots with no collectives in this library; see "
-              "DESIGN.md for how it would shard.", file=sys.stderr)
+              "objective path is data-parallel over slots, so each GPU would run it on its own share of "
+              "the anchor blocks and only the four pooled metric sums would be all-reduced; this library "
+              "has no collectives.", file=sys.stderr)
         sys.exit(2)
     if args.config not in WORKLOADS:
         print(f"config {args.config} is not available in this build", file=sys.stderr)
