@@ -77,8 +77,8 @@ KERNEL_NAMES = [
     (r"sum_partials_kernel", "dprev_reduce"),
     (r"gather_rows_kernel", "markov_gather"),
     (r"dw2_kernel", "markov_dw2"),
-    (r"markov_keys_kernel", "markov_sort"),
-    (r"markov_scatter_kernel", "markov_scatter"),
+    (r"markov_(?:sort_chunks|merge)_kernel", "markov_sort"),
+    (r"markov_(?:pieces|runs)_kernel", "markov_scatter"),
     (r"rms_fwd_kernel", "rms_norm_fwd"),
     (r"rms_bwd_kernel", "rms_norm_bwd"),
     (r"rms_wgrad_kernel", "rms_norm_wgrad"),
@@ -172,8 +172,6 @@ def stats_summary(directory: str, config: str, command: str) -> str:
     other = 0.0
     for r in rows:
         name = timer_name(r["Name"])
-        if not name and "rocprim::" in r["Name"]:
-            name = "markov_sort"   # the radix sort the library launches through hipCUB / rocPRIM
         if not name:
             other += float(r["Percentage"])
             continue

@@ -192,6 +192,27 @@ def rows_2d(t: torch.Tensor, cols: int) -> tuple[torch.Tensor, int]:
     return t2, ld
 
 
+def pow2_ratio(emitted: int, wanted: int):
+    """emitted / wanted when it is a power of two (1/4, 2, ...), else None.  dl is linear in
+    1/accumulation_steps, and every rounding on its way commutes with a power-of-two scale, so
+    dl emitted for `emitted` steps times this ratio is, bit for bit, the dl emitted for `wanted`
+    (for normal values; a result below 2^-126 can differ in its last bits)."""
+    from fractions import Fraction
+
+    f = Fraction(int(emitted), int(wanted))
+    if f.numerator & (f.numerator - 1) == 0 and f.denominator & (f.denominator - 1) == 0:
+        return float(f)
+    return None
+
+
+def scale_inplace(t: torch.Tensor, factor: float) -> None:
+    """t *= factor on the device (ns_scale_gradient), t contiguous bf16 or fp32."""
+    if not t.is_contiguous():
+        raise ValueError("scale_inplace needs a contiguous tensor")
+    f = torch.full((), float(factor), dtype=torch.float32, device=t.device)
+    check(load().ns_scale_gradient(ptr(t), dtype_code(t), t.numel(), ptr(f), stream(t.device)), "ns_scale_gradient")
+
+
 class KernelTimer:
     """Context manager around ns_profile_begin/end: per-kernel launches and
     total milliseconds, measured with HIP events on each launch's stream."""

@@ -20,8 +20,10 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kQBlock = 128;     // quantisation block (K) and weight-scale block (rows, K)
 
-// float in [-448, 448] -> OCP e4m3 (fn) code, round to nearest even; -0 keeps its sign.
+// float in [-448, 448] or NaN -> OCP e4m3 (fn) code, round to nearest even; -0 keeps its
+// sign; NaN gives the NaN code 0x7F (the sign of a NaN carries nothing).
 __device__ __forceinline__ uint32_t e4m3_code(float x) {
+  if (x != x) return 0x7Fu;
   const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
   const float a = fabsf(x);
   uint32_t code;
@@ -35,7 +37,13 @@ __device__ __forceinline__ uint32_t e4m3_code(float x) {
   return code | sign;
 }
 
-// One wave per (row, 128-block): lane l owns elements 2l, 2l+1.
+// torch's clamp keeps a NaN (fminf / fmaxf would replace it by the bound)
+__device__ __forceinline__ float clamp448(float q) { return q != q ? q : fminf(fmaxf(q, -448.0f), 448.0f); }
+
+// One wave per (row, 128-block): lane l owns elements 2l, 2l+1.  Non-finite inputs follow
+// the reference's tensor ops: a NaN makes the block's amax, so its scale and every code,
+// NaN; an infinity makes the scale inf, the finite entries' codes +-0 and its own code NaN
+// (inf / inf).  Either way the block dequantises to NaN and so do the row's logits.
 __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t n,
                                                         int64_t d, uint8_t* __restrict__ q,
                                                         float* __restrict__ xs) {
@@ -49,10 +57,13 @@ __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restri
   float amax = fmaxf(fabsf(x0), fabsf(x1));
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  // abs().amax() propagates a NaN, which fmaxf drops
+  if (__any((x0 != x0) || (x1 != x1))) amax = __builtin_nanf("");
   const float s = __fdiv_rn(amax, 448.0f);
-  const float den = fmaxf(s, 1.17549435e-38f);   // clamp_min(torch.finfo(float32).tiny)
-  const float q0 = fminf(fmaxf(__fdiv_rn(x0, den), -448.0f), 448.0f);
-  const float q1 = fminf(fmaxf(__fdiv_rn(x1, den), -448.0f), 448.0f);
+  // clamp_min(torch.finfo(float32).tiny), keeping a NaN scale
+  const float den = s != s ? s : fmaxf(s, 1.17549435e-38f);
+  const float q0 = clamp448(__fdiv_rn(x0, den));
+  const float q1 = clamp448(__fdiv_rn(x1, den));
   const uint16_t codes = (uint16_t)(e4m3_code(q0) | (e4m3_code(q1) << 8));
   *reinterpret_cast<uint16_t*>(q + row * d + kb * kQBlock + 2 * lane) = codes;
   if (lane == 0) xs[row * nb + kb] = s;

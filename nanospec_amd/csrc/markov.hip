@@ -3,10 +3,10 @@
 //   w2.grad     = dl^T . w1[prev]            ops.linear_backward, dw (copied, not accumulated)
 //   w1.grad    += index_add(prev, d(prev))   ops.embedding_backward (ops.py:73-74)
 // d(previous) comes out of the dh GEMM as extra column tiles (lmhead_backward_ext);
-// w2.grad is a K = N GEMM with both operands K-major; the index_add sorts (prev, t) with
-// a stable radix sort and lets one wave per distinct id sum that id's rows in token order,
+// w2.grad is a K = N GEMM with both operands K-major; the index_add sorts (prev, t) pairs
+// (a bitonic chunk sort and merge passes, below) and sums each id's rows in a fixed order,
 // so the result does not depend on scheduling (the reference's GPU index_add_ does).
-#include <hipcub/hipcub.hpp>
+#include <utility>
 
 #include "ns_gemm.h"
 #include "ns_internal.h"
@@ -171,35 +171,126 @@ void dw2_kernel(Dw2Params p) {
     }
 }
 
-// Sort keys: the row of w1 each token's d(previous) goes to (V for ids outside [0, V):
-// they sort last and are skipped), paired with the token index.
-__global__ __launch_bounds__(256) void markov_keys_kernel(const int64_t* __restrict__ prev, int64_t n, int64_t v,
-                                                          uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n) return;
-  const int64_t id = prev[t];
-  keys[t] = (id >= 0 && id < v) ? (uint32_t)id : (uint32_t)v;
-  vals[t] = (uint32_t)t;
+// ---- w1.grad.index_add_(prev, d(previous)), deterministic -------------------------------
+// Each token's d(previous) row goes to w1.grad row prev[t].  The pairs are sorted by the
+// composite key (row << 32) | t: the keys are unique, so any correct sort is the stable
+// sort by row, and a row's tokens come out in token order.  Ids outside [0, V) get row V
+// (sorted after every real row, skipped); padding up to a whole sort chunk gets row
+// 0xFFFFFFFF (after those).  The sum of each row's d(previous) rows is then formed in two
+// levels so that one frequent id does not serialise the step: fixed segments of kSeg
+// sorted positions sum the pieces of the runs they hold (token order), and one wave per
+// run adds the run's pieces in segment order and adds the result to w1.grad with one
+// rounding.  Every order is fixed, so the result does not depend on scheduling.
+constexpr int kSortChunk = 4096;   // keys per workgroup sorted in LDS (32 KB)
+constexpr int kSortThreads = 1024;
+constexpr int kSeg = 64;           // sorted positions per piece segment (one wave)
+
+int64_t sort_padded(int64_t n) { return (n + kSortChunk - 1) / kSortChunk * kSortChunk; }
+
+// Build the keys of one chunk and bitonic-sort it in LDS (ascending).
+__global__ __launch_bounds__(kSortThreads) void markov_sort_chunks_kernel(const int64_t* __restrict__ prev, int64_t n,
+                                                                         int64_t v, uint64_t* __restrict__ out) {
+  __shared__ uint64_t sk[kSortChunk];
+  const int64_t base = (int64_t)blockIdx.x * kSortChunk;
+  for (int i = threadIdx.x; i < kSortChunk; i += kSortThreads) {
+    const int64_t t = base + i;
+    uint64_t k;
+    if (t < n) {
+      const int64_t id = prev[t];
+      const uint64_t row = (id >= 0 && id < v) ? (uint64_t)id : (uint64_t)v;
+      k = (row << 32) | (uint64_t)t;
+    } else {
+      k = (0xFFFFFFFFull << 32) | (uint64_t)t;
+    }
+    sk[i] = k;
+  }
+  __syncthreads();
+  for (int size = 2; size <= kSortChunk; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int q = threadIdx.x; q < kSortChunk / 2; q += kSortThreads) {
+        // pair q: element i with bit `stride` clear and its partner i + stride
+        const int i = (q / stride) * 2 * stride + (q % stride);
+        const int j = i + stride;
+        const bool up = (i & size) == 0;
+        const uint64_t a = sk[i], b = sk[j];
+        if ((a > b) == up) {
+          sk[i] = b;
+          sk[j] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < kSortChunk; i += kSortThreads) out[base + i] = sk[i];
 }
 
-// One wave per sorted position; the first position of each id sums that id's rows of
-// d(previous) in token order (fp32) and adds the sum into w1.grad's row (bf16).
-__global__ __launch_bounds__(256) void markov_scatter_kernel(const uint32_t* __restrict__ keys,
-                                                             const uint32_t* __restrict__ vals, int64_t n, int64_t v,
-                                                             int64_t r, const float* __restrict__ dprev,
-                                                             uint16_t* __restrict__ w1g, int64_t ldg1) {
+// Merge sorted runs of length len pairwise (runs 2m and 2m + 1) from src into dst, n_pad
+// keys: a key's place is its position in its run plus the number of the other run's keys
+// below it (a binary search; the keys are unique).  A run without a partner stays put.
+__global__ __launch_bounds__(256) void markov_merge_kernel(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
+                                                           int64_t n_pad, int64_t len) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_pad) return;
+  const uint64_t x = src[i];
+  const int64_t run = i / len, pos = i - run * len;
+  const int64_t other = (run ^ 1) * len;
+  int64_t olen = n_pad - other;
+  olen = olen < 0 ? 0 : (olen > len ? len : olen);
+  int64_t lo = 0, hi = olen;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (src[other + mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  dst[(run & ~int64_t(1)) * len + pos + lo] = x;
+}
+
+// One wave per segment of kSeg sorted positions: the fp32 sum, in sorted (token) order, of
+// each run piece the segment holds, stored at the piece's first position.
+__global__ __launch_bounds__(256) void markov_pieces_kernel(const uint64_t* __restrict__ keys, int64_t n, int64_t v,
+                                                            int64_t r, const float* __restrict__ dprev,
+                                                            float* __restrict__ piece) {
+  const int64_t s0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kSeg;
+  if (s0 >= n) return;
+  const int lane = threadIdx.x & 63;
+  const int cnt = n - s0 < kSeg ? (int)(n - s0) : kSeg;
+  const uint64_t km = lane < cnt ? keys[s0 + lane] : ~0ull;
+  const int row_m = (int)(uint32_t)(km >> 32), tok_m = (int)(uint32_t)km;
+  for (int64_t c = lane * 4; c < r; c += 256) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int start = 0;
+    for (int j = 0; j < cnt; ++j) {
+      const int row = __shfl(row_m, j), tok = __shfl(tok_m, j);
+      const float4 x = *reinterpret_cast<const float4*>(dprev + (int64_t)tok * r + c);
+      acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
+      const int next = __shfl(row_m, j + 1 < cnt ? j + 1 : j);
+      if (j + 1 == cnt || next != row) {
+        if ((uint32_t)row < (uint64_t)v) *reinterpret_cast<float4*>(piece + (s0 + start) * r + c) = acc;
+        acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        start = j + 1;
+      }
+    }
+  }
+}
+
+// One wave per sorted position; the first position of each row adds the row's pieces
+// (its own, then one per following segment it spans, in order) into w1.grad's row with one
+// rounding to bf16.
+__global__ __launch_bounds__(256) void markov_runs_kernel(const uint64_t* __restrict__ keys, int64_t n, int64_t v,
+                                                          int64_t r, const float* __restrict__ piece,
+                                                          uint16_t* __restrict__ w1g, int64_t ldg1) {
   const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= n) return;
-  const uint32_t key = keys[i];
-  if (key >= (uint32_t)v || (i > 0 && keys[i - 1] == key)) return;
+  const uint64_t row = keys[i] >> 32;
+  if (row >= (uint64_t)v || (i > 0 && (keys[i - 1] >> 32) == row)) return;
   const int lane = threadIdx.x & 63;
   for (int64_t c = lane * 4; c < r; c += 256) {
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int64_t j = i; j < n && keys[j] == key; ++j) {
-      const float4 x = *reinterpret_cast<const float4*>(dprev + (int64_t)vals[j] * r + c);
+    float4 s = *reinterpret_cast<const float4*>(piece + i * r + c);
+    for (int64_t q = (i / kSeg + 1) * kSeg; q < n && (keys[q] >> 32) == row; q += kSeg) {
+      const float4 x = *reinterpret_cast<const float4*>(piece + q * r + c);
       s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
     }
-    uint16_t* g = w1g + (int64_t)key * ldg1 + c;
+    uint16_t* g = w1g + (int64_t)row * ldg1 + c;
     const uint2 old = *reinterpret_cast<const uint2*>(g);
     uint2 o;
     o.x = pack_bf16x2(bf16_lo(old.x) + s.x, bf16_hi(old.x) + s.y);
@@ -208,50 +299,29 @@ __global__ __launch_bounds__(256) void markov_scatter_kernel(const uint32_t* __r
   }
 }
 
-int key_bits(int64_t v) {
-  int b = 1;
-  while (b < 32 && (int64_t(1) << b) <= v) ++b;
-  return b;
-}
-
-size_t sort_temp_bytes(int64_t n, int64_t v) {
-  size_t bytes = 0;
-  const hipError_t e = hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, static_cast<const uint32_t*>(nullptr),
-                                                          static_cast<uint32_t*>(nullptr),
-                                                          static_cast<const uint32_t*>(nullptr),
-                                                          static_cast<uint32_t*>(nullptr), (int)n, 0, key_bits(v));
-  // without a device the query cannot run; a generous bound keeps the size defined
-  return e == hipSuccess ? bytes : (size_t)16 * n * 4 + (size_t(16) << 20);
-}
-
 struct MarkovWs {
   void* dh_ws;
   float* dprev;
   uint16_t* e;
-  uint32_t *keys_in, *keys_out, *vals_in, *vals_out;
-  void* sort_tmp;
-  size_t sort_bytes;
+  uint64_t *keys_a, *keys_b;   // sort ping-pong, sort_padded(n) each
+  float* piece;                // [n, r] run-piece sums
 };
 
 size_t markov_ws_layout(int64_t n, int64_t v, int64_t d, int64_t r, void* base, MarkovWs* w) {
   const size_t b_dh = align_up(lmhead_bwd_workspace_bytes(n, v, d, r, true), 256);
   const size_t b_dp = align_up((size_t)n * r * sizeof(float), 256);
   const size_t b_e = align_up((size_t)n * r * 2, 256);
-  const size_t b_k = align_up((size_t)n * 4, 256);
-  const size_t b_s = align_up(sort_temp_bytes(n, v), 256);
+  const size_t b_k = align_up((size_t)sort_padded(n) * sizeof(uint64_t), 256);
   if (w) {
     char* p = static_cast<char*>(base);
     w->dh_ws = p; p += b_dh;
     w->dprev = reinterpret_cast<float*>(p); p += b_dp;
     w->e = reinterpret_cast<uint16_t*>(p); p += b_e;
-    w->keys_in = reinterpret_cast<uint32_t*>(p); p += b_k;
-    w->keys_out = reinterpret_cast<uint32_t*>(p); p += b_k;
-    w->vals_in = reinterpret_cast<uint32_t*>(p); p += b_k;
-    w->vals_out = reinterpret_cast<uint32_t*>(p); p += b_k;
-    w->sort_tmp = p;
-    w->sort_bytes = b_s;
+    w->keys_a = reinterpret_cast<uint64_t*>(p); p += b_k;
+    w->keys_b = reinterpret_cast<uint64_t*>(p); p += b_k;
+    w->piece = reinterpret_cast<float*>(p);
   }
-  return b_dh + b_dp + b_e + 4 * b_k + b_s;
+  return b_dh + b_dp + b_e + 2 * b_k + b_dp;
 }
 
 }  // namespace
@@ -295,17 +365,24 @@ hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int6
   }
   {
     NS_TIMED("markov_sort", st);
-    hipLaunchKernelGGL(markov_keys_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, f.prev, n, v,
-                       w.keys_in, w.vals_in);
+    const int64_t n_pad = sort_padded(n);
+    hipLaunchKernelGGL(markov_sort_chunks_kernel, dim3((unsigned)(n_pad / kSortChunk)), dim3(kSortThreads), 0, st,
+                       f.prev, n, v, w.keys_a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    size_t tmp = w.sort_bytes;
-    if ((e = hipcub::DeviceRadixSort::SortPairs(w.sort_tmp, tmp, w.keys_in, w.keys_out, w.vals_in, w.vals_out, (int)n,
-                                                0, key_bits(v), st)) != hipSuccess)
-      return e;
+    for (int64_t len = kSortChunk; len < n_pad; len *= 2) {
+      hipLaunchKernelGGL(markov_merge_kernel, dim3((unsigned)((n_pad + 255) / 256)), dim3(256), 0, st, w.keys_a,
+                         w.keys_b, n_pad, len);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      std::swap(w.keys_a, w.keys_b);
+    }
   }
   NS_TIMED("markov_scatter", st);
-  hipLaunchKernelGGL(markov_scatter_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, w.keys_out, w.vals_out, n,
-                     v, r, w.dprev, static_cast<uint16_t*>(w1_grad), ldg1);
+  const int64_t segs = (n + kSeg - 1) / kSeg;
+  hipLaunchKernelGGL(markov_pieces_kernel, dim3((unsigned)((segs + 3) / 4)), dim3(256), 0, st, w.keys_a, n, v, r,
+                     w.dprev, w.piece);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(markov_runs_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, w.keys_a, n, v, r, w.piece,
+                     static_cast<uint16_t*>(w1_grad), ldg1);
   (void)ws_bytes;
   return hipGetLastError();
 }

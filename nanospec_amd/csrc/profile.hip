@@ -1,6 +1,7 @@
 // Opt-in kernel timing: while enabled, every library launch is bracketed by a
 // pair of HIP events recorded on the launch stream; ns_profile_end() waits for
 // them and reports per-kernel launch counts and total milliseconds.
+#include <atomic>
 #include <mutex>
 #include <string.h>
 #include <string>
@@ -19,7 +20,8 @@ struct Record {
 };
 
 std::mutex g_mu;
-bool g_on = false;
+// read without the mutex on every launch (profiling()), written under it
+std::atomic<bool> g_on{false};
 std::vector<Record> g_records;
 std::vector<hipEvent_t> g_pool;
 
@@ -36,11 +38,11 @@ hipEvent_t take_event() {
 
 }  // namespace
 
-bool profiling() { return g_on; }
+bool profiling() { return g_on.load(std::memory_order_acquire); }
 
 void* profile_start(const char* name, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
-  if (!g_on) return nullptr;
+  if (!g_on.load(std::memory_order_relaxed)) return nullptr;
   Record r{name, take_event(), take_event(), hipSuccess};
   if (!r.start || !r.stop || hipEventRecord(r.start, st) != hipSuccess) {
     if (r.start) g_pool.push_back(r.start);
@@ -64,13 +66,13 @@ extern "C" {
 
 int ns_profile_begin(void) {
   std::lock_guard<std::mutex> lk(ns::g_mu);
-  ns::g_on = true;
+  ns::g_on.store(true, std::memory_order_release);
   return NS_OK;
 }
 
 int ns_profile_end(ns_kernel_time* out, int capacity, int* count) {
   std::lock_guard<std::mutex> lk(ns::g_mu);
-  ns::g_on = false;
+  ns::g_on.store(false, std::memory_order_release);
   std::vector<std::string> names;
   std::vector<ns_kernel_time> acc;
   int status = NS_OK;

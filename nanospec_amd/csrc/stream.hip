@@ -18,13 +18,6 @@
 #include "ns_internal.h"
 #include "ns_profile.h"
 
-#ifndef NS_EMIT_UNROLL
-#define NS_EMIT_UNROLL 1
-#endif
-#ifndef NS_EMIT_NT
-#define NS_EMIT_NT 1
-#endif
-
 namespace ns {
 
 constexpr int kStreamThreads = 256;
@@ -275,18 +268,12 @@ __global__ __launch_bounds__(kStreamThreads) void stream_emit_kernel(
             for (int e = 0; e < 8; ++e)
               if (i0 + e == y) d[e] -= cy;
           }
-#if NS_EMIT_NT
-          store8_nt(dr + i0, d);
-#else
-          store8(dr + i0, d);
-#endif
+          store8_nt(dr + i0, d);   // dl is not read back by this pass: keep z, u in cache
         }
       }
     };
     int64_t j = threadIdx.x;
-#if NS_EMIT_UNROLL
     for (; j + kStreamThreads < nvec; j += 2 * kStreamThreads) body(std::integral_constant<int, 2>{}, j);
-#endif
     for (; j < nvec; j += kStreamThreads) body(std::integral_constant<int, 1>{}, j);
     scalar_from = lo + nvec * 8;
   }

@@ -230,8 +230,11 @@ def _reemit_dlogits(saved: HeadActivations, accumulation_steps: int) -> torch.Te
 
 
 def _markov_inputs(markov: MarkovFactors, vocab: int, n: int, device):
-    """Flatten and check the factored Markov head's inputs."""
-    prev = markov.previous.reshape(-1).to(device=device, dtype=torch.int64).contiguous()
+    """Flatten and check the factored Markov head's inputs: all three on ``device`` (the
+    kernels take their raw pointers, so a host tensor is refused here, not copied)."""
+    if _lib.require_device(markov.previous, markov.w1, markov.w2) != device:
+        raise ValueError(f"markov factors live on {markov.w1.device}, the head's operands on {device}")
+    prev = markov.previous.reshape(-1).to(dtype=torch.int64).contiguous()
     if prev.numel() != n:
         raise ValueError(f"markov.previous has {prev.numel()} entries, hidden has {n} rows")
     if markov.w1.dim() != 2 or markov.w2.dim() != 2 or markov.w1.shape != markov.w2.shape:
@@ -345,21 +348,26 @@ def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, retu
                            markov_grads=None, final_norm=None):
     """dh = dl . W_lm (train.py:301-302).  Returns dh [..., d] bf16 (and dl [..., V] bf16
     when ``return_dlogits``, for the Markov backward).  dl is the one the forward emitted
-    when it was emitted for this ``accumulation_steps``; otherwise (another value,
-    ``emit_dlogits=False``, or a second backward) pass 2 runs again from the saved row
-    statistics, giving the bits a forward with this value emits.
+    when it was emitted for this ``accumulation_steps``, or that dl scaled in place when the
+    two counts differ by a power of two (bit-identical to an emission for this count, for
+    normal values); otherwise (another count, ``emit_dlogits=False``, or a second backward)
+    pass 2 runs again from the saved row statistics, giving the bits a forward with this
+    count emits.
     ``markov_grads=(w1_grad, w2_grad)`` with a factored Markov forward also runs the
     Markov-head backward in the same GEMM (``lm_head_markov_backward``).
     ``final_norm=(RMSActivations, norm weight, norm weight grad)`` fuses final_norm's
     backward into the dh reduction and returns dx in place of dh (train.py:308-310)."""
     if accumulation_steps < 1:
         raise ValueError("accumulation_steps must be >= 1")
-    if saved.dlogits is not None and accumulation_steps == saved.accumulation_steps:
-        dl = saved.dlogits
-    else:
-        saved.dlogits = None
+    dl, saved.dlogits = saved.dlogits, None   # handed over once, so it is freed after dh unless returned
+    if dl is not None and accumulation_steps != saved.accumulation_steps:
+        ratio = _lib.pow2_ratio(saved.accumulation_steps, accumulation_steps)
+        if ratio is not None:
+            _lib.scale_inplace(dl, ratio)   # the bits an emission for this count has
+        else:
+            dl = None
+    if dl is None:
         dl = _reemit_dlogits(saved, accumulation_steps)
-    saved.dlogits = None   # handed over once, so it is freed after dh unless returned
     if markov_grads is not None:
         if saved.markov is None:
             raise ValueError("markov_grads given, but the forward ran without Markov factors")

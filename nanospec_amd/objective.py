@@ -99,7 +99,9 @@ def ce_kl_loss(logits, target_logits, prepared, objective, *, accumulation_steps
     A target id of -100 is F.cross_entropy's ignore_index: that row has no CE term.  Any
     other id outside [0, V) makes the loss NaN (the reference raises; the device cannot).
     Keyword extensions: ``accumulation_steps`` pre-scales the dl emitted with the
-    forward; ``emit_dlogits=False`` skips it (metrics only).
+    forward (default 1: the reference passes the count to ce_kl_backward only, and a
+    power-of-two count there rescales this dl in place); ``emit_dlogits=False`` skips it
+    (metrics only).
     """
     o = objective
     if logits.shape != target_logits.shape:
@@ -134,11 +136,22 @@ def ce_kl_loss(logits, target_logits, prepared, objective, *, accumulation_steps
 
 @torch.no_grad()
 def ce_kl_backward(saved, accumulation_steps=1):
-    """dl in the logits dtype (objective.py:70-80)."""
-    if saved.dlogits is not None and accumulation_steps == saved.emitted_steps:
+    """dl in the logits dtype (objective.py:70-80).
+
+    The dl the forward emitted (for its ``accumulation_steps``, 1 by default, as
+    train.py:291 calls ce_kl_loss) is handed over when the counts match.  When they differ
+    by a power of two (the reference passes the count only here, train.py:301), that dl is
+    scaled in place, which gives the bits the forward would have emitted for this count.
+    Any other count, or a second backward, runs the emit pass again."""
+    if saved.dlogits is not None:
         dl, saved.dlogits = saved.dlogits, None
-        return dl
-    saved.dlogits = None
+        if accumulation_steps == saved.emitted_steps:
+            return dl
+        ratio = _lib.pow2_ratio(saved.emitted_steps, accumulation_steps)
+        if ratio is not None:
+            _lib.scale_inplace(dl, ratio)
+            return dl
+        del dl
     o = saved.objective
     logits, target = saved.logits, saved.target_logits
     device = _lib.require_device(logits, target)

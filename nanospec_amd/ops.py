@@ -134,7 +134,10 @@ def rms_norm(x, weight, eps):
 
 
 def norm_args(saved: RMSActivations, weight, weight_grad, dx):
-    """The C struct ns_rms_norm_args for a saved rms_norm; returns (struct, keep-alive)."""
+    """The C struct ns_rms_norm_args for a saved rms_norm; returns (struct, keep-alive).
+    Every tensor whose pointer goes into the struct must be on dx's device."""
+    if _lib.require_device(saved.input, saved.inverse_rms, weight, weight_grad, dx) != dx.device:
+        raise ValueError(f"rms-norm operands live on {saved.input.device}, dx on {dx.device}")
     d = saved.input.shape[-1]
     x, ldx = _lib.rows_2d(saved.input, d)
     if x.dtype != torch.bfloat16:

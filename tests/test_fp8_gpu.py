@@ -147,3 +147,36 @@ def test_c4_teacher_once_with_fp8_lse(gpu_lib):
     rs = _np(s1.row_stats)[rows]
     np.testing.assert_allclose(rs[:, 2], r["ce"], rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(rs[:, 3], r["kl"], rtol=1e-4, atol=1e-4)
+
+
+def test_non_finite_activations_poison_their_rows(gpu_lib):
+    """A NaN (or inf) activation: the block's scale and codes as the reference's tensor ops
+    leave them (NaN codes of either sign count alike), and that row's logits and log-sum-exp
+    NaN while every other row matches the finite result."""
+    g = torch.Generator(device=DEV).manual_seed(21)
+    n, d, v = 64, 256, 1024
+    x = torch.randn((n, d), generator=g, device=DEV).bfloat16()
+    x[1, 5] = float("nan")
+    x[2, 130] = float("-inf")
+    q, xs = ops.fp8_quantize_rows(x)
+    torch.cuda.synchronize()
+    with np.errstate(invalid="ignore"):
+        q_ref, xs_ref = ref.quantize_activation_blocks(_np(x))
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+    qn = q.cpu().numpy()
+    nan_code = (q_ref & 0x7F) == 0x7F
+    np.testing.assert_array_equal((qn & 0x7F) == 0x7F, nan_code)
+    np.testing.assert_array_equal(qn[~nan_code], q_ref[~nan_code])
+    w = 0.02 * torch.randn((v, d), generator=g, device=DEV)
+    blocks = w.view(v // 128, 128, d // 128, 128)
+    scale = blocks.abs().amax(dim=(1, 3)) / 448.0
+    codes = (blocks / scale[:, None, :, None]).clamp(-448, 448).reshape(v, d).to(torch.float8_e4m3fn)
+    spec = ops.fp8_teacher_logits(x, codes, scale)
+    torch.cuda.synchronize()
+    out = _np(spec.logits)
+    assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
+    lse = _np(spec.lse)
+    assert np.isnan(lse[1]) and np.isnan(lse[2])
+    good = np.r_[0, 3:n]
+    assert np.isfinite(out[good]).all() and np.isfinite(lse[good]).all()
+    _assert_fp8_logits(out[good], _np(x[good]), codes.view(torch.uint8).cpu().numpy(), scale.cpu().numpy())

@@ -126,3 +126,22 @@ def test_empty_batch(gpu_lib):
     torch.cuda.synchronize()
     assert dh.shape == (0, 8, d)
     assert float(m.denominator) == 0.0 and float(m.loss) == 0.0 and float(m.accept_len_total) == 0.0
+
+
+@pytest.mark.parametrize("kind", ["dense", "factored"])
+@pytest.mark.parametrize("fwd_steps,bwd_steps", [(1, 4), (4, 2), (2, 8)])
+def test_power_of_two_steps_rescale_the_emitted_dl(gpu_lib, kind, fwd_steps, bwd_steps):
+    """The reference passes accumulation_steps to the backward only (train.py:291, 301): a
+    forward that emitted dl for one count and a backward for another differing by a power of
+    two scale the emitted dl in place, with the bits a forward for that count emits."""
+    hidden, weight, target, slots, kw, _ = _case(kind)
+    o = Objective(block_size=8)
+    _, s_want = head.lm_head_ce_kl_loss(hidden, weight, target, slots, o, accumulation_steps=bwd_steps, **kw)
+    want = s_want.dlogits.clone()
+    _, saved = head.lm_head_ce_kl_loss(hidden, weight, target, slots, o, accumulation_steps=fwd_steps, **kw)
+    emitted = saved.dlogits
+    dh, dl = head.lm_head_ce_kl_backward(saved, bwd_steps, return_dlogits=True)
+    torch.cuda.synchronize()
+    assert dl.data_ptr() == emitted.data_ptr()          # scaled in place, pass 2 not rerun
+    assert torch.equal(dl.reshape(want.shape), want)
+    assert torch.equal(dh, head.lm_head_ce_kl_backward(s_want, bwd_steps))

@@ -194,3 +194,22 @@ def test_markov_forward_backward_through_head_step(gpu_lib):
     _assert_grads(dl2, mk, g1, w1_grad, w2_grad)
     sim = ref.similarity(_np(dh).reshape(n, d), ref.lm_head_backward(_np(dl2), _np(weight)))
     assert sim["cosine_min"] >= 0.9999, sim
+
+
+@pytest.mark.parametrize("n,hot", [
+    (8192, 4096),     # two sort chunks and one merge pass; one id on half the rows
+    (12288, 12000),   # three chunks (a run with no merge partner); one id on almost every row
+])
+def test_markov_backward_skewed_ids(gpu_lib, n, hot):
+    """A skewed previous-token distribution, as dropped anchor blocks give (every slot of a
+    dropped block takes the block's first id, dspark.py:120-127): `hot` rows share one id.
+    w1.grad matches the oracle and is bitwise reproducible."""
+    v, d, r = 4096, 128, 256
+    dl, w, mk, g1 = _bwd_inputs(n, v, d, r, 90 + n)
+    g = torch.Generator(device=DEV).manual_seed(n)
+    hot_rows = torch.randperm(n, generator=g, device=DEV)[:hot]
+    mk.previous[hot_rows] = 17
+    a = _run_bwd(dl, w, mk, g1)
+    b = _run_bwd(dl, w, mk, g1)
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    _assert_grads(dl, mk, g1, a[1], a[2])

@@ -220,3 +220,26 @@ def test_c1_full_size(gpu_lib):
     assert float((row_sum / row_abs).max()) < 1e-2
     masked = ~slots.valid.reshape(-1)
     assert torch.count_nonzero(dl[masked]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_power_of_two_steps_rescale_the_emitted_dl(gpu_lib, dtype):
+    """ce_kl_loss emits dl for its accumulation_steps (1 when the caller passes none, as
+    train.py:291 does); ce_kl_backward(saved, 4) then scales it in place, with the bits the
+    forward would have emitted for 4; a count that is not a power-of-two multiple (3) runs the
+    emit pass again."""
+    z, u, slots = synthetic.logits_inputs(32, 4096, 16, DEV)
+    z, u = z.to(dtype), u.to(dtype)
+    o = Objective(block_size=8)
+    _, s4 = nobj.ce_kl_loss(z, u, slots, o, accumulation_steps=4)
+    want = nobj.ce_kl_backward(s4, 4)
+    _, saved = nobj.ce_kl_loss(z, u, slots, o)
+    emitted = saved.dlogits
+    dl = nobj.ce_kl_backward(saved, 4)
+    torch.cuda.synchronize()
+    assert dl.data_ptr() == emitted.data_ptr() and torch.equal(dl, want)
+    _, saved = nobj.ce_kl_loss(z, u, slots, o)
+    dl3 = nobj.ce_kl_backward(saved, 3)
+    _, s3 = nobj.ce_kl_loss(z, u, slots, o, accumulation_steps=3)
+    torch.cuda.synchronize()
+    assert torch.equal(dl3, nobj.ce_kl_backward(s3, 3))

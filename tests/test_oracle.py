@@ -305,6 +305,37 @@ def test_fp8_linear_matches_torch_float8_semantics():
     np.testing.assert_array_equal(ref.fp8_linear(x, wc, s), lib)
 
 
+def _torch_activation_codes(x):
+    """ops.py:189-196 as torch tensor ops: (codes, scales) of x [n, d]."""
+    xb = torch.from_numpy(x).reshape(x.shape[0], -1, 128)
+    xs = xb.abs().amax(-1, keepdim=True) / 448.0
+    q = (xb / xs.clamp_min(torch.finfo(torch.float32).tiny)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).reshape(x.shape).numpy(), xs[..., 0].numpy()
+
+
+def test_fp8_non_finite_activation_poisons_its_row():
+    """A NaN activation makes its block's scale and codes NaN, an infinity makes the scale
+    inf and its own code NaN (inf / inf), as torch's amax / clamp / float8 cast do; either
+    way that row's logits are NaN and the other rows are untouched."""
+    g = np.random.default_rng(20)
+    n, d, v = 4, 256, 256
+    x = ref.bf16_round(g.standard_normal((n, d)).astype(np.float32))
+    x[1, 5] = np.nan
+    x[2, 130] = -np.inf
+    codes, xs = ref.quantize_activation_blocks(x)
+    t_codes, t_xs = _torch_activation_codes(x)
+    np.testing.assert_array_equal(xs, t_xs)          # NaN at [1, 0], inf at [2, 1]
+    nan_code = (codes & 0x7F) == 0x7F
+    np.testing.assert_array_equal(nan_code, (t_codes & 0x7F) == 0x7F)   # NaN codes of either sign
+    np.testing.assert_array_equal(codes[~nan_code], t_codes[~nan_code])
+    assert nan_code[1, :128].all() and nan_code[2].sum() == 1
+    wc, s = ref.quantize_weight_blocks((0.02 * g.standard_normal((v, d))).astype(np.float32))
+    with np.errstate(invalid="ignore"):
+        out = ref.fp8_linear(x, wc, s)
+    assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
+    assert np.isfinite(out[[0, 3]]).all()
+
+
 # ------------------------------------------------------------ slot preparation
 
 
