@@ -8,7 +8,8 @@ input that is already resident in HBM.
 
     python bench.py [--steps K] [--warmup W] [--config c1|c2|c2x|c3|c4]
 
-Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a
+Prints ONE JSON line.  By default the headline is C2 (the configuration the metric is
+quoted on) and C1 and C4 follow in the same process under "secondary".  One GPU only: ``--gpus N`` with N > 1 exits with a
 message (the path is data-parallel over slots; the library has no collectives).
 """
 
@@ -33,7 +34,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c2x"])
+    p.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c4", "c2x"],
+                   help="one workload alone; default: C2 (the headline) and then C1 and C4 as secondary lines")
+    p.add_argument("--no-secondary", action="store_true", help="default run: C2 only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU-baseline sample (0: default)")
     p.add_argument("--pmc-driver", action="store_true",
@@ -41,6 +44,8 @@ def parse():
     p.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="print the HBM-traffic summary of two --pmc-driver passes (FETCH_SIZE, WRITE_SIZE)")
     p.add_argument("--stats-from", metavar="DIR", help="print a summary of a rocprofv3 --stats csv run")
+    p.add_argument("--mfma-from", metavar="DIR",
+                   help="print the matrix-core summary of one --pmc-driver pass with the MFMA counters")
     p.add_argument("--command", default="", help="command line recorded in a printed summary")
     return p.parse_args()
 
@@ -201,6 +206,157 @@ def committed_traffic(config: str, kernel: str):
     return int(m.group(1)) + int(m.group(2)), os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
 
 
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_VALU_MFMA_BUSY_CYCLES",
+                 "GRBM_GUI_ACTIVE")
+SIMDS = 1024                        # MI355X: 256 CUs x 4 SIMDs
+FLOP_PER_CLK_SIMD = {"bf16": 1024.0, "fp8": 2048.0}   # dense MFMA: 2.5 (5.0) PFLOP/s at 2.4 GHz
+
+
+def _per_dispatch(directory: str):
+    """{dispatch id: (kernel name, {counter: value})} of one --pmc pass, plus
+    {dispatch id: duration ns} from the same run's kernel trace."""
+    counters = {}
+    for r in _csv_rows(directory, "counter_collection.csv"):
+        d = int(r["Dispatch_Id"])
+        counters.setdefault(d, (r["Kernel_Name"], {}))[1][r["Counter_Name"]] = float(r["Counter_Value"])
+    durations = {}
+    for r in _csv_rows(directory, "kernel_trace.csv"):
+        durations[int(r["Dispatch_Id"])] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    return counters, durations
+
+
+def mfma_summary(directory: str, config: str, command: str) -> str:
+    """Markdown: the matrix cores of each library GEMM kernel from one rocprofv3 pass with
+    MFMA_COUNTERS and --kernel-trace (per-dispatch medians):
+    * executed FLOP = MOPS x 512 (bf16 or fp8), to check against the algorithmic count;
+    * clock = GRBM_GUI_ACTIVE / duration, where GRBM_GUI_ACTIVE is summed over the 8 XCDs
+      (so it is divided by 8);
+    * mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1024 SIMDs);
+    * per_clock = executed FLOP / (cycles x 1024 SIMDs x dense FLOP per SIMD per clock): the
+      fraction of the matrix cores' peak at the clock the chip actually ran."""
+    import statistics
+
+    counters, durations = _per_dispatch(directory)
+    per = {}
+    for d, (kname, vals) in counters.items():
+        name = timer_name(kname)
+        if not name or d not in durations or not all(c in vals for c in MFMA_COUNTERS):
+            continue
+        bf, f8 = vals["SQ_INSTS_VALU_MFMA_MOPS_BF16"], vals["SQ_INSTS_VALU_MFMA_MOPS_F8"]
+        if bf + f8 == 0:
+            continue
+        dtype = "fp8" if f8 > bf else "bf16"
+        flop = 512.0 * (f8 if dtype == "fp8" else bf)
+        dur = durations[d] * 1e-9
+        cycles = vals["GRBM_GUI_ACTIVE"] / 8.0
+        per.setdefault(name, []).append(dict(
+            dtype=dtype, flop=flop, ms=dur * 1e3, clock_GHz=cycles / dur / 1e9,
+            mfma_busy=vals["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * SIMDS),
+            per_clock=flop / (cycles * SIMDS * FLOP_PER_CLK_SIMD[dtype]),
+            peak_frac=flop / dur / (2.5e15 if dtype == "bf16" else 5.0e15)))
+    if not per:
+        raise SystemExit(f"no library MFMA dispatches with {MFMA_COUNTERS} in {directory}")
+    out = [f"# Matrix cores per GEMM kernel: {config.upper()} (rocprofv3 MFMA counters)", "",
+           "Command (from the repository root on the MI355X box):", "", "```", command.strip(), "```", "",
+           "One `bench.py --pmc-driver` pass (one step, a calibration copy, two steps) with "
+           f"`--pmc {' '.join(MFMA_COUNTERS)} --kernel-trace`; per-dispatch medians. FLOP executed = "
+           "`SQ_INSTS_VALU_MFMA_MOPS_*` x 512. Clock = `GRBM_GUI_ACTIVE` / 8 XCDs / kernel duration. "
+           "MFMA busy = `SQ_VALU_MFMA_BUSY_CYCLES` / (cycles x 1024 SIMDs). Per-clock = FLOP / (cycles x 1024 "
+           "SIMDs x dense FLOP per SIMD per clock: 1024 bf16, 2048 fp8), the fraction of the matrix cores' "
+           "peak at the clock the chip ran. Peak fraction = FLOP / duration / (2.5 PFLOP/s bf16, 5.0 fp8), "
+           "against the published 2.4 GHz figure.", "",
+           "| kernel | dtype | dispatches | duration ms | TFLOP executed | clock GHz | MFMA busy | per-clock | "
+           "of dense peak |", "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    machine = []
+    for name in sorted(per):
+        rows = per[name]
+        med = {k: statistics.median(r[k] for r in rows) for k in ("flop", "ms", "clock_GHz", "mfma_busy",
+                                                                 "per_clock", "peak_frac")}
+        out.append(f"| `{name}` | {rows[0]['dtype']} | {len(rows)} | {med['ms']:.3f} | {med['flop'] / 1e12:.2f} | "
+                   f"{med['clock_GHz']:.2f} | {med['mfma_busy']:.3f} | {med['per_clock']:.3f} | "
+                   f"{med['peak_frac']:.3f} |")
+        machine.append(f"mfma {name} dtype={rows[0]['dtype']} flop={med['flop']:.0f} clock_GHz={med['clock_GHz']:.3f} "
+                       f"mfma_busy={med['mfma_busy']:.4f} per_clock={med['per_clock']:.4f}")
+    out += ["", "Machine-readable (read by bench.py into `roofline`):", "", "```"] + machine + ["```", ""]
+    return "\n".join(out)
+
+
+def committed_mfma(config: str, kernel: str):
+    """{mfma_busy, clock_GHz, mfma_per_clock, mfma_source} of `kernel` from the committed
+    matrix-core summary, or None."""
+    import re
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{PROFILE_PREFIX[config]}_mfma.md")
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(rf"^mfma {re.escape(kernel)} dtype=\w+ flop=\d+ clock_GHz=([\d.]+) mfma_busy=([\d.]+) "
+                  rf"per_clock=([\d.]+)$", text, re.M)
+    if not m:
+        return None
+    return {"clock_GHz": float(m.group(1)), "mfma_busy": float(m.group(2)), "mfma_per_clock": float(m.group(3)),
+            "mfma_source": os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))}
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+
+def cpu_threads() -> int:
+    """Host threads of the CPU baseline: the job's CPU share (OMP_NUM_THREADS, 16 on the GPU
+    box) when set, at most os.cpu_count()."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def time_cpu(run, reps: int = 3):
+    """BASELINE's timing plan for the CPU leg: one untimed warmup, then `reps` timed
+    repetitions; returns (median seconds, all timings)."""
+    import statistics
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def cpu_report(rows, n, med, times, threads, what, extra=""):
+    """The cpu_baseline object: slots/s of a whole-block sample.  Every [N, V] operation is
+    row-local and accept_len is block-local, so the sample's rate is the full batch's rate."""
+    import torch
+
+    return dict(value=rows / med, unit="slots/s", cores=threads, kind="port",
+                sample=(f"numpy fp32 oracle (oracle/objective_ref.py), {what}, on {rows} of the {n} rows "
+                        f"({rows // 8} whole blocks; every [N,V] op is row-local and accept_len block-local, so the "
+                        f"sample's slots/s is the full batch's). 1 warmup + {len(times)} timed repetitions, median "
+                        f"{med:.2f} s (all: {', '.join(f'{t:.2f}' for t in times)} s){extra}"),
+                threads={"used": threads, "os_cpu_count": os.cpu_count(), "torch_get_num_threads": torch.get_num_threads(),
+                         "cpu_model": cpu_model()})
+
+
+def oracle_backward(ref, z, u, w, y, o, threads):
+    """ce_kl_backward of the oracle over row chunks on `threads` host threads (row-local)."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+
+    out = np.empty(z.shape, dtype=np.float32)
+
+    def chunk(lo):
+        hi = min(z.shape[0], lo + 16)
+        out[lo:hi] = ref.ce_kl_backward(z[lo:hi], u[lo:hi], w[lo:hi], y[lo:hi], o.ce, o.kl, 1, dtype=np.float32)
+
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(chunk, range(0, z.shape[0], 16)))
+    return out
+
+
 # --------------------------------------------------------------------------- C1
 
 
@@ -228,24 +384,27 @@ def workload_c1(device, args):
 
     def cpu_baseline(rows):
         import numpy as np
+        from threadpoolctl import threadpool_limits
 
         from oracle import objective_ref as ref
 
-        rows = rows or n
+        rows = rows or 2048   # about 10-20 s of host work with warmup and 3 repetitions
+        threads = cpu_threads()
         zs = z[:rows].float().cpu().numpy()
         us = u[:rows].float().cpu().numpy()
         w = slots.weights.reshape(-1)[:rows].cpu().numpy()
         y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
         vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
-        t0 = time.perf_counter()
-        ref.ce_kl_loss(zs, us, w.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
-                       dtype=np.float32, chunk_rows=32)
-        ref.ce_kl_backward(zs, us, w, y, o.ce, o.kl, 1, dtype=np.float32)
-        dt = time.perf_counter() - t0
-        return dict(value=rows / dt, unit="slots/s", cores=1, kind="port",
-                    sample=f"numpy fp32 oracle (oracle/objective_ref.py), single thread, {rows} of the "
-                           f"{n} C1 rows ({rows // 8} whole blocks), V={v}: ce_kl_loss + ce_kl_backward; "
-                           f"{dt:.2f} s")
+
+        def run():
+            ref.ce_kl_loss(zs, us, w.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
+                           dtype=np.float32, chunk_rows=16, workers=threads)
+            oracle_backward(ref, zs, us, w, y, o, threads)
+
+        with threadpool_limits(limits=threads, user_api="blas"):
+            med, times = time_cpu(run)
+        return cpu_report(rows, n, med, times, threads,
+                          f"ce_kl_loss + ce_kl_backward, row chunks on {threads} threads, V={v}")
 
     config = {"workload": "C1 logits-only: CE+KL+accept fwd + dlogits bwd over given bf16 [N,V] logits",
               "N": n, "V": v, "K": 8, "gamma": 4.0, "masked_rows": int((~slots.valid).sum()),
@@ -263,7 +422,8 @@ def workload_c1(device, args):
                 "read2_write1_ms": rw, "read2_write1_GBs": 3 * b / (rw / 1e3) / 1e9}
 
     return dict(step=step, n=n, per_slot_bytes=per_slot, per_slot_flops=None, kernel_bytes=kernel_bytes,
-                kernel_flops={}, cpu_baseline=cpu_baseline, config=config, dtype="bf16", ceilings=ceilings,
+                kernel_flops={}, stream_kernels=("stream_stats", "stream_emit"), cpu_baseline=cpu_baseline,
+                config=config, dtype="bf16", ceilings=ceilings,
                 inputs={"draft_logits": z, "teacher_logits": u, "weights": slots.weights,
                         "target_ids": slots.target_ids, "valid": slots.valid})
 
@@ -310,16 +470,19 @@ def workload_head(device, args, which):
 
     def cpu_baseline(rows):
         import numpy as np
-        from threadpoolctl import threadpool_info
+        from threadpoolctl import threadpool_limits
 
         from oracle import objective_ref as ref
 
-        # about 10 s of host work at C2 / C4 (whole blocks of 8)
-        rows = rows or (1024 if fp8 is not None else 2560)
-        t_copy = time.perf_counter()
+        rows = rows or (1024 if fp8 is not None else 1536)   # about 10-20 s with warmup and 3 repetitions
+        threads = cpu_threads()
         w32 = weight.float().cpu().numpy()
         hs = hidden[:rows].float().cpu().numpy()
         ms = markov[:rows].float().cpu().numpy()
+        wt = slots.weights.reshape(-1)[:rows].cpu().numpy()
+        y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
+        vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
+        fixed = None
         if fp8 is not None:
             xt, codes, scale = fp8
             xq = xt[:rows].float().cpu().numpy()
@@ -327,24 +490,31 @@ def workload_head(device, args, which):
             sc = scale.cpu().numpy()
         else:
             us = teacher[:rows].float().cpu().numpy()
-        wt = slots.weights.reshape(-1)[:rows].cpu().numpy()
-        y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
-        vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
-        t_copy = time.perf_counter() - t_copy
-        t0 = time.perf_counter()
-        if fp8 is not None:
-            us = ref.fp8_linear(xq, wc, sc, dtype=np.float32)
-        z = ref.lm_head_logits(hs, w32, ms, dtype=np.float32)
-        ref.ce_kl_loss(z, us, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
-                       dtype=np.float32, chunk_rows=16)
-        dl = ref.ce_kl_backward(z, us, wt, y, o.ce, o.kl, 1, dtype=np.float32).astype(np.float32)
-        ref.lm_head_backward(dl, w32, dtype=np.float32)
-        dt = time.perf_counter() - t0
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-        return dict(value=rows / dt, unit="slots/s", cores=threads, kind="port",
-                    sample=f"numpy fp32 oracle (oracle/objective_ref.py): {rows} of the {n} {which.upper()} rows "
-                           f"({rows // 8} whole blocks), d={d}, V={v}: LM-head GEMM (BLAS, {threads} threads), "
-                           f"ce_kl_loss, ce_kl_backward, dh GEMM; {dt:.2f} s (weight copy {t_copy:.1f} s untimed)")
+
+        def run():
+            u = ref.fp8_linear(xq, wc, sc, dtype=np.float32) if fp8 is not None else us
+            z = ref.lm_head_logits(hs, w32, ms, dtype=np.float32)
+            ref.ce_kl_loss(z, u, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
+                           dtype=np.float32, chunk_rows=16, workers=threads)
+            dl = oracle_backward(ref, z, u, wt, y, o, threads)
+            ref.lm_head_backward(dl, w32, dtype=np.float32)
+
+        with threadpool_limits(limits=threads, user_api="blas"):
+            med, times = time_cpu(run)
+            if fp8 is not None:
+                # fp8_linear dequantises the whole weight on every call (ops.py:198-199), a cost per
+                # batch, not per slot: time it alone and charge it once per N-row batch
+                fixed, _ = time_cpu(lambda: ref.fp8_linear(xq[:8], wc, sc, dtype=np.float32), reps=1)
+        extra = ""
+        if fixed is not None:
+            per_row = max(med - fixed, 1e-9) / rows
+            med_full = fixed + per_row * n
+            extra = (f"; the weight dequantisation ({fixed:.2f} s) is charged once per {n}-row batch: "
+                     f"{med_full:.1f} s per batch")
+            med = med_full * rows / n
+        return cpu_report(rows, n, med, times, threads,
+                          f"{'fp8_linear teacher head, ' if fp8 is not None else ''}LM-head GEMM (BLAS), "
+                          f"ce_kl_loss, ce_kl_backward, dh GEMM; d={d}, V={v}; {threads} threads", extra)
 
     name = {"c2": "C2 full fused", "c3": "C3 long-batch", "c4": "C4 FP8 teacher head + full fused"}[which]
     config = {"workload": f"{name}: LM-head GEMM + Markov addend + CE+KL+accept fwd, dl + dhidden bwd",
@@ -418,12 +588,12 @@ def workload_c2x(device, args):
 
     def cpu_baseline(rows):
         import numpy as np
-        from threadpoolctl import threadpool_info
+        from threadpoolctl import threadpool_limits
 
         from oracle import objective_ref as ref
 
-        rows = rows or 2048   # about 10 s of host work
-        t_copy = time.perf_counter()
+        rows = rows or 1024
+        threads = cpu_threads()
         w32 = weight.float().cpu().numpy()
         w1n, w2n = w1.float().cpu().numpy(), w2.float().cpu().numpy()
         xs = x[:rows].float().cpu().numpy()
@@ -433,23 +603,22 @@ def workload_c2x(device, args):
         wt = slots.weights.reshape(-1)[:rows].cpu().numpy()
         y = slots.target_ids.reshape(-1)[:rows].cpu().numpy()
         vv = slots.valid.reshape(-1)[:rows].cpu().numpy()
-        t_copy = time.perf_counter() - t_copy
-        t0 = time.perf_counter()
-        hs, inv, _ = ref.rms_norm(xs, wn, 1e-6)
-        z = ref.lm_head_logits(hs, w32, dtype=np.float32) + ref.markov_logits(pv, w1n, w2n, dtype=np.float32)
-        ref.ce_kl_loss(z, us, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
-                       dtype=np.float32, chunk_rows=16)
-        dl = ref.ce_kl_backward(z, us, wt, y, o.ce, o.kl, 1, dtype=np.float32).astype(np.float32)
-        dh = ref.bf16_round(ref.lm_head_backward(dl, w32, dtype=np.float32))
-        ref.rms_norm_backward(dh, xs, inv, wn)
-        ref.markov_backward(dl, pv, w1n, w2n, dtype=np.float32)
-        dt = time.perf_counter() - t0
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-        return dict(value=rows / dt, unit="slots/s", cores=threads, kind="port",
-                    sample=f"numpy fp32 oracle (oracle/objective_ref.py): {rows} of the {n} C2X rows "
-                           f"({rows // 8} whole blocks), d={d}, V={v}, r={r}: rms_norm, LM-head + Markov GEMMs "
-                           f"(BLAS, {threads} threads), ce_kl_loss, ce_kl_backward, dh GEMM, rms_norm backward, "
-                           f"Markov backward; {dt:.2f} s (weight copy {t_copy:.1f} s untimed)")
+
+        def run():
+            hs, inv, _ = ref.rms_norm(xs, wn, 1e-6)
+            z = ref.lm_head_logits(hs, w32, dtype=np.float32) + ref.markov_logits(pv, w1n, w2n, dtype=np.float32)
+            ref.ce_kl_loss(z, us, wt.reshape(-1, 8), y.reshape(-1, 8), vv.reshape(-1, 8), o.ce, o.kl,
+                           dtype=np.float32, chunk_rows=16, workers=threads)
+            dl = oracle_backward(ref, z, us, wt, y, o, threads)
+            dh = ref.bf16_round(ref.lm_head_backward(dl, w32, dtype=np.float32))
+            ref.rms_norm_backward(dh, xs, inv, wn)
+            ref.markov_backward(dl, pv, w1n, w2n, dtype=np.float32)
+
+        with threadpool_limits(limits=threads, user_api="blas"):
+            med, times = time_cpu(run)
+        return cpu_report(rows, n, med, times, threads,
+                          f"rms_norm, LM-head + Markov GEMMs (BLAS), ce_kl_loss, ce_kl_backward, dh GEMM, rms_norm "
+                          f"backward, Markov backward; d={d}, V={v}, r={r}; {threads} threads")
 
     config = {"workload": "C2X: C2 with final_norm around the head, the factored Markov head (r=256) fused "
                           "as a second K segment, and the pooled tail; fwd, dl + dx + final_norm / markov_w1 / "
@@ -522,42 +691,18 @@ def pmc_driver(step, device):
     print("pmc driver: done", flush=True)
 
 
-def main():
-    args = parse()
-    if args.traffic_from:
-        print(traffic_summary(args.traffic_from[0], args.traffic_from[1], args.config, args.command))
-        return
-    if args.stats_from:
-        print(stats_summary(args.stats_from, args.config, args.command))
-        return
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the "
-              "objective path is data-parallel over slots, so each GPU would run it on its own share of "
-              "the anchor blocks and only the four pooled metric sums would be all-reduced; this library "
-              "has no collectives.", file=sys.stderr)
-        sys.exit(2)
-    if args.config not in WORKLOADS:
-        print(f"config {args.config} is not available in this build", file=sys.stderr)
-        sys.exit(2)
-
+def measure(wl, args, config_name):
+    """Warmup, then exactly `args.steps` timed steps of workload `wl` between two device
+    synchronisations; per-kernel means from the library's own HIP-event timer in the same
+    window; the dominant kernel's roofline."""
     import torch
 
     from nanospec_amd import _lib
 
-    device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    _lib.load()
-    wl = WORKLOADS[args.config](device, args)
     step = wl["step"]
-    if args.pmc_driver:
-        pmc_driver(step, device)
-        return
-
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-
     # timed window: exactly K steps between two device synchronisations.  Kernel
     # durations come from HIP events the library records around each of its launches,
     # on the stream the launch uses, inside this same window.
@@ -576,23 +721,33 @@ def main():
     n = wl["n"]
     value = n * args.steps / (gpu_ms / 1e3)
     kernels = {name: {"launches": c, "mean_ms": tot / max(c, 1)} for name, (c, tot) in kt.times.items()}
-    dominant = max(kt.times, key=lambda k: kt.times[k][1])
-    dom_ms = kernels[dominant]["mean_ms"]
-    if dominant in wl["kernel_flops"]:
-        achieved = wl["kernel_flops"][dominant] / (dom_ms / 1e3) / 1e12
-        roof = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / BF16_PEAK_TFLOPS}
-    else:
-        achieved = wl["kernel_bytes"].get(dominant, 0) / (dom_ms / 1e3) / 1e9
-        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS}
-    roof["kernel"] = dominant
-    roof["kernel_mean_ms"] = dom_ms
-    tr = committed_traffic(args.config, dominant)
-    roof["traffic"] = tr[0] if tr else None
-    if tr:
-        roof["traffic_source"] = tr[1]
     fp8_flops = wl.get("kernel_fp8_flops", {})
+
+    def roofline(kernel):
+        k_ms = kernels[kernel]["mean_ms"]
+        if kernel in wl["kernel_flops"] or kernel in fp8_flops:
+            fp8 = kernel in fp8_flops
+            peak = FP8_PEAK_TFLOPS if fp8 else BF16_PEAK_TFLOPS
+            achieved = (fp8_flops if fp8 else wl["kernel_flops"])[kernel] / (k_ms / 1e3) / 1e12
+            roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                    "frac": achieved / peak, "dtype": "fp8" if fp8 else "bf16"}
+        else:
+            achieved = wl["kernel_bytes"].get(kernel, 0) / (k_ms / 1e3) / 1e9
+            roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBS}
+        roof["kernel"] = kernel
+        roof["kernel_mean_ms"] = k_ms
+        tr = committed_traffic(config_name, kernel)
+        roof["traffic"] = tr[0] if tr else None
+        if tr:
+            roof["traffic_source"] = tr[1]
+        mf = committed_mfma(config_name, kernel)
+        if mf:
+            roof.update(mf)
+        return roof
+
+    dominant = max(kt.times, key=lambda k: kt.times[k][1])
+    roof = roofline(dominant)
     for name, info in kernels.items():
         if name in wl["kernel_bytes"]:
             info["algorithmic_GBs"] = wl["kernel_bytes"][name] / (info["mean_ms"] / 1e3) / 1e9
@@ -613,35 +768,95 @@ def main():
         if wl.get("per_slot_fp8_flops"):
             ideal_s += wl["per_slot_fp8_flops"] * n / (FP8_PEAK_TFLOPS * 1e12)
         step_roof["mfma_frac"] = ideal_s / (ms_per_step / 1e3)
+    out = {"value": value, "unit": "slots/s", "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms_per_step, "dtype": wl["dtype"], "config": wl["config"], "roofline": roof,
+           "step_roofline": step_roof, "kernels": kernels, "wall_s": wall}
+    # every kernel the north star sets a target for: the HBM stream kernels and the GEMMs
+    out["rooflines"] = {k: roofline(k) for k in kernels
+                        if k in wl["kernel_flops"] or k in fp8_flops or k in wl.get("stream_kernels", ())}
+    return out
 
+
+def main():
+    args = parse()
+    if args.traffic_from:
+        print(traffic_summary(args.traffic_from[0], args.traffic_from[1], args.config, args.command))
+        return
+    if args.stats_from:
+        print(stats_summary(args.stats_from, args.config, args.command))
+        return
+    if args.mfma_from:
+        print(mfma_summary(args.mfma_from, args.config, args.command))
+        return
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the "
+              "objective path is data-parallel over slots, so each GPU would run it on its own share of "
+              "the anchor blocks and only the four pooled metric sums would be all-reduced; this library "
+              "has no collectives.", file=sys.stderr)
+        sys.exit(2)
+    headline = args.config or "c2"
+    if headline not in WORKLOADS:
+        print(f"config {headline} is not available in this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from nanospec_amd import _lib
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    _lib.load()
+    wl = WORKLOADS[headline](device, args)
+    if args.pmc_driver:
+        pmc_driver(wl["step"], device)
+        return
+
+    res = measure(wl, args, headline)
     # practical ceilings measured with library kernels in this run (context for roofline)
     ceil = wl["ceilings"]() if "ceilings" in wl else None
-
     cpu = None
     if not args.no_cpu_baseline:
         cpu = wl["cpu_baseline"](args.cpu_rows)
+    inputs_sha = {k: sample_sha256(t) for k, t in wl.get("inputs", {}).items() if t is not None}
+    del wl
+    torch.cuda.empty_cache()
+
+    # the other configurations whose targets the north star names, in the same process:
+    # C1 (the logit stream against HBM) and C4 (the fp8 teacher head); each its own steps
+    secondary = {}
+    if args.config is None and not args.no_secondary:
+        for name in ("c1", "c4"):
+            wl2 = WORKLOADS[name](device, args)
+            r2 = measure(wl2, args, name)
+            r2["inputs_sha256"] = {k: sample_sha256(t) for k, t in wl2.get("inputs", {}).items() if t is not None}
+            secondary[name] = r2
+            del wl2
+            torch.cuda.empty_cache()
 
     line = {
         "metric": METRIC,
-        "value": value,
+        "value": res["value"],
         "unit": "slots/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": wl["dtype"],
+        "dtype": res["dtype"],
         "data": "synthetic (seeded; distributions of BASELINE.json configs)",
-        "config": wl["config"],
-        "roofline": roof,
-        "step_roofline": step_roof,
-        "kernels": kernels,
+        "config": res["config"],
+        "roofline": res["roofline"],
+        "step_roofline": res["step_roofline"],
+        "rooflines": res["rooflines"],
+        "kernels": res["kernels"],
         "cpu_baseline": cpu,
         "library_ceilings": ceil,
-        "wall_s": wall,
-        "inputs_sha256": {k: sample_sha256(t) for k, t in wl.get("inputs", {}).items() if t is not None},
+        "wall_s": res["wall_s"],
+        "inputs_sha256": inputs_sha,
+        "secondary": secondary or None,
         "host": {"cpu_model": cpu_model(), "cpu_count": os.cpu_count()},
         "device": torch.cuda.get_device_name(device),
     }

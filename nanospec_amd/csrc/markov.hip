@@ -256,16 +256,22 @@ __global__ __launch_bounds__(256) void markov_pieces_kernel(const uint64_t* __re
   const int cnt = n - s0 < kSeg ? (int)(n - s0) : kSeg;
   const uint64_t km = lane < cnt ? keys[s0 + lane] : ~0ull;
   const int row_m = (int)(uint32_t)(km >> 32), tok_m = (int)(uint32_t)km;
-  for (int64_t c = lane * 4; c < r; c += 256) {
+  // the column loop is uniform over the wave (its shuffles need every lane); lanes past r
+  // only skip their loads and stores
+  for (int64_t cb = 0; cb < r; cb += 256) {
+    const int64_t c = cb + lane * 4;
+    const bool act = c < r;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     int start = 0;
     for (int j = 0; j < cnt; ++j) {
       const int row = __shfl(row_m, j), tok = __shfl(tok_m, j);
-      const float4 x = *reinterpret_cast<const float4*>(dprev + (int64_t)tok * r + c);
-      acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
       const int next = __shfl(row_m, j + 1 < cnt ? j + 1 : j);
+      if (act) {
+        const float4 x = *reinterpret_cast<const float4*>(dprev + (int64_t)tok * r + c);
+        acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
+      }
       if (j + 1 == cnt || next != row) {
-        if ((uint32_t)row < (uint64_t)v) *reinterpret_cast<float4*>(piece + (s0 + start) * r + c) = acc;
+        if (act && (uint32_t)row < (uint64_t)v) *reinterpret_cast<float4*>(piece + (s0 + start) * r + c) = acc;
         acc = make_float4(0.f, 0.f, 0.f, 0.f);
         start = j + 1;
       }

@@ -242,12 +242,15 @@ def acceptance_length_counts(accept_rate, valid):
     return float((lengths * block_valid).sum()), float(block_valid.sum())
 
 
-def ce_kl_loss(z, u, weights, labels, valid, c_ce=0.1, c_kl=0.9, dtype=np.float64, chunk_rows=64):
+def ce_kl_loss(z, u, weights, labels, valid, c_ce=0.1, c_kl=0.9, dtype=np.float64, chunk_rows=64, workers=1):
     """Forward objective: the six LossMetrics plus per-row statistics.
 
     z, u [N, V] (or [..., K, V]); weights, labels, valid [..., K] with N rows in
     blocks of K consecutive slots.  Follows
     objective.py:49-67 and the LossMetrics properties at objective.py:20-26.
+    Every row statistic is row-local, so chunks of ``chunk_rows`` rows may run on
+    ``workers`` host threads (numpy releases the GIL inside its loops); the sums over
+    rows are then taken in row order as with one worker.
     """
     valid = np.asarray(valid)
     if valid.ndim < 2:
@@ -259,11 +262,21 @@ def ce_kl_loss(z, u, weights, labels, valid, c_ce=0.1, c_kl=0.9, dtype=np.float6
     z = np.asarray(z).reshape(n, -1)
     u = np.asarray(u).reshape(n, -1)
     rows = {key: np.empty(n, dtype=np.float64) for key in ("lse_z", "lse_u", "ce", "kl", "accept_rate")}
-    for lo in range(0, n, chunk_rows):
+
+    def chunk(lo):
         hi = min(n, lo + chunk_rows)
         part = row_objective(z[lo:hi], u[lo:hi], labels[lo:hi], dtype=dtype)
         for key in rows:
             rows[key][lo:hi] = part[key]
+
+    if workers > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=workers) as ex:
+            list(ex.map(chunk, range(0, n, chunk_rows)))
+    else:
+        for lo in range(0, n, chunk_rows):
+            chunk(lo)
     den = float(weights.sum())
     ce_sum = float((rows["ce"] * weights).sum())
     kl_sum = float((rows["kl"] * weights).sum())

@@ -1,0 +1,295 @@
+"""Full-batch parity at the benchmark configurations, measured directly against the fp32
+oracle (objective.py:49-80 with ops.py:183-200 for C4's teacher and train.py:302 for dh).
+
+* C1, C2, C4: every row through the chunked fp32 oracle.  The six LossMetrics, loss and
+  accept_len agree to 1e-4 relative, and every row's statistics agree as well.  dl and dh are
+  compared on 64 whole blocks (512 rows).  C4 runs the backward after the fp8 teacher head,
+  and the oracle's teacher is ``fp8_linear`` on the same codes.
+* C3 (N = 32,768): row statistics, dl and dh on 512 whole blocks (4096 rows).  On every row,
+  the metrics are checked against the kernel's own row statistics, along with the
+  size-independent properties.
+* Near agreement at full V: the teacher is the draft's own logits plus N(0, 0.5^2) noise.
+  Accept rates are then 0.5-0.9, and KL = A/s_u - lse_u + lse_z cancels terms of 12-17 down
+  to about 0.1.  The same 1e-4 bar applies.
+
+dhidden bar (north star): on every row, max |dh - dh_ref| <= 2e-2 max |dh_ref| and cosine
+>= 0.9999.  dl bar: one bf16 ulp plus the fp32 evaluation error where (c_ce + c_kl) p and
+c_kl t cancel.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from nanospec_amd import head, ops, synthetic
+from nanospec_amd import objective as nobj
+from nanospec_amd.config import Objective
+from oracle import objective_ref as ref
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+DEV = "cuda:0"
+WORKERS = max(1, min(16, os.cpu_count() or 1))
+FIELDS = ("ce", "kl", "numerator", "denominator", "accept_len_sum", "accept_len_total")
+K = 8
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _metrics(m):
+    out = {f: float(getattr(m, f)) for f in FIELDS}
+    out["loss"] = float(m.loss)
+    out["accept_len"] = float(m.accept_len)
+    return out
+
+
+def _assert_metrics(got, want, rel=1e-4):
+    for key in FIELDS + ("loss", "accept_len"):
+        w = want[key]
+        assert got[key] == pytest.approx(w, rel=rel, abs=1e-6 * max(1.0, abs(w))), (key, got[key], w)
+
+
+def _slot_arrays(slots, rows=None):
+    w = _np(slots.weights).reshape(-1)
+    y = slots.target_ids.reshape(-1).cpu().numpy()
+    v = slots.valid.reshape(-1).cpu().numpy()
+    if rows is not None:
+        w, y, v = w[rows], y[rows], v[rows]
+    return w, y, v
+
+
+def _oracle_rows(z, u, slots, o, rows=None):
+    """Oracle metrics and row statistics (fp32, row chunks on host threads)."""
+    w, y, v = _slot_arrays(slots, rows)
+    return ref.ce_kl_loss(z, u, w.reshape(-1, K), y.reshape(-1, K), v.reshape(-1, K), o.ce, o.kl,
+                          dtype=np.float32, chunk_rows=16, workers=WORKERS)
+
+
+def _assert_rows(rs, want):
+    np.testing.assert_allclose(rs[:, 0], want["lse_z"], rtol=5e-6, atol=1e-4)
+    np.testing.assert_allclose(rs[:, 1], want["lse_u"], rtol=5e-6, atol=1e-4)
+    np.testing.assert_allclose(rs[:, 2], want["ce"], rtol=2e-5, atol=1e-4)
+    np.testing.assert_allclose(rs[:, 3], want["kl"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(rs[:, 4], want["accept_rate"], atol=2e-5)
+
+
+def _assert_dl(dl_gpu, dl_ref):
+    """One bf16 ulp, plus fp32 evaluation error where the terms of dl cancel; 64 rows at a time."""
+    for i in range(0, dl_ref.shape[0], 64):
+        g = dl_gpu[i:i + 64].astype(np.float64)
+        w = dl_ref[i:i + 64].astype(np.float64)
+        tol = np.abs(w) * 2.0 ** -7 + 2e-5 * np.abs(w).max(axis=-1, keepdims=True)
+        assert np.all(np.abs(g - w) <= tol), (i, float((np.abs(g - w) - tol).max()))
+
+
+def _assert_dh_rows(dh_gpu, dh_ref):
+    """Per row: max error <= 2e-2 of the row's largest |dh| and cosine >= 0.9999; rows whose
+    reference is exactly zero (masked slots) are exactly zero."""
+    g = dh_gpu.astype(np.float64)
+    w = dh_ref.astype(np.float64)
+    rmax = np.abs(w).max(-1)
+    live = rmax > 0
+    assert np.all(g[~live] == 0.0)
+    err = np.abs(g - w).max(-1)[live] / rmax[live]
+    assert err.max() <= 2e-2, float(err.max())
+    cos = (g * w).sum(-1)[live] / (np.linalg.norm(g, axis=-1)[live] * np.linalg.norm(w, axis=-1)[live])
+    assert cos.min() >= 0.9999, float(cos.min())
+
+
+def _blocks(nb, count):
+    """Rows of `count` whole blocks spread evenly over nb blocks."""
+    b = np.unique(np.linspace(0, nb - 1, count).astype(np.int64))
+    return (b[:, None] * K + np.arange(K)[None, :]).reshape(-1)
+
+
+def _head_z(hidden, w32, markov, rows=None):
+    h = _np(hidden if rows is None else hidden[torch.as_tensor(rows, device=DEV)])
+    z = h @ w32.T
+    if markov is not None:
+        z += _np(markov if rows is None else markov[torch.as_tensor(rows, device=DEV)])
+    return z
+
+
+def _check_head(hidden, weight, markov, target, u_ref, slots, o, dl_blocks=64, u_dl=None):
+    """Run the fused forward and backward on `target`, then compare with the oracle on every
+    row (u_ref: the oracle's teacher logits for every row, fp32).  dl and dh are the
+    objective's derivative of the teacher the GPU path consumed: u_dl (default u_ref)."""
+    m, saved = head.lm_head_ce_kl_loss(hidden, weight, target, slots, o, markov_logits=markov)
+    dh, dl = head.lm_head_ce_kl_backward(saved, return_dlogits=True)
+    torch.cuda.synchronize()
+    n = hidden.shape[0]
+    w32 = _np(weight)
+    z = _head_z(hidden, w32, markov)
+    m_ref, rows_ref = _oracle_rows(z, u_ref, slots, o)
+    _assert_metrics(_metrics(m), m_ref)
+    rs = _np(saved.row_stats)
+    _assert_rows(rs, rows_ref)
+    y = slots.target_ids.reshape(-1).cpu().numpy()
+    np.testing.assert_allclose(rs[:, 5], z[np.arange(n), y], rtol=1e-5, atol=1e-4)
+    _assert_row_properties(rs, dl, dh, weight, slots)
+    rows = _blocks(n // K, dl_blocks)
+    w, yy, _ = _slot_arrays(slots, rows)
+    u_dl = u_ref if u_dl is None else u_dl
+    dl_ref = ref.ce_kl_backward(z[rows], u_dl[rows], w, yy, o.ce, o.kl, dtype=np.float32).astype(np.float32)
+    del z
+    _assert_dl(_np(dl.reshape(n, -1)[torch.as_tensor(rows, device=DEV)]), dl_ref)
+    dh_ref = ref.lm_head_backward(dl_ref, w32, dtype=np.float32)
+    _assert_dh_rows(_np(dh.reshape(n, -1)[torch.as_tensor(rows, device=DEV)]), dh_ref)
+    return m_ref, rows_ref
+
+
+def test_c1_every_row(gpu_lib):
+    """C1 (N = 4096, V = 248,320, 10% of rows masked): the six metrics of the whole batch and
+    every row's statistics against the oracle; dl on 64 whole blocks."""
+    z, u, slots = synthetic.c1(DEV)
+    o = Objective(block_size=K)
+    m, saved = nobj.ce_kl_loss(z, u, slots, o)
+    dl = nobj.ce_kl_backward(saved)
+    torch.cuda.synchronize()
+    zn, un = _np(z), _np(u)
+    m_ref, rows_ref = _oracle_rows(zn, un, slots, o)
+    _assert_metrics(_metrics(m), m_ref)
+    _assert_rows(_np(saved.row_stats), rows_ref)
+    rows = _blocks(z.shape[0] // K, 64)
+    w, y, _ = _slot_arrays(slots, rows)
+    dl_ref = ref.ce_kl_backward(zn[rows], un[rows], w, y, o.ce, o.kl, dtype=np.float32)
+    _assert_dl(_np(dl[torch.as_tensor(rows, device=DEV)]), dl_ref)
+
+
+def test_c2_every_row(gpu_lib):
+    """C2 (N = 4096, d = 5120, V = 248,320): every row, the metrics of the whole batch, and dl
+    and dh on 64 whole blocks."""
+    hidden, weight, markov, teacher, slots = synthetic.c2(DEV)
+    _check_head(hidden, weight, markov, teacher, _np(teacher), slots, Objective(block_size=K))
+
+
+def test_c4_every_row_after_the_fp8_teacher(gpu_lib):
+    """C4: the fp8 teacher head (ops.fp8_linear numerics, its LSE from the epilogue) feeding
+    the fused objective and its backward; the oracle's teacher is fp8_linear on the same
+    codes and scales for every row."""
+    hidden, weight, markov, (xt, codes, scale), slots = synthetic.c4(DEV)
+    spec = ops.fp8_teacher_logits(xt, codes.view(torch.float8_e4m3fn), scale)
+    torch.cuda.synchronize()
+    cn, sn = codes.cpu().numpy(), scale.cpu().numpy()
+    u_ref = ref.fp8_linear(_np(xt), cn, sn, dtype=np.float32)
+    u_gpu = _np(spec.logits)
+    # the teacher logits themselves on 64 whole blocks: the fp8 bound of test_fp8_gpu.py
+    rows = _blocks(xt.shape[0] // K, 64)
+    _assert_fp8_bound(u_gpu[rows], _np(xt)[rows], cn, sn)
+    # the metrics end to end (oracle teacher); dl and dh on the teacher the objective consumed
+    _check_head(hidden, weight, markov, spec, u_ref, slots, Objective(block_size=K), u_dl=u_gpu)
+
+
+def _assert_fp8_bound(got, x, codes, scale):
+    """fp8 teacher logits: |got - exact| <= half a bf16 ulp of the exact value (the output
+    rounding) + 2^-14 sum_k |x_k w_k| (the matrix core's accumulation inside 128-entry K
+    blocks), and at least 98% equal to the correctly rounded exact value.  Exact in fp64,
+    over V in chunks."""
+    q, xs = ref.quantize_activation_blocks(x)
+    dx = (ref.e4m3_decode(q).reshape(q.shape[0], -1, 128) * xs[..., None]).astype(np.float32)
+    dx = dx.reshape(q.shape).astype(np.float64)
+    same, total, worst = 0, 0, 0.0
+    for v0 in range(0, codes.shape[0], 16384):
+        c = codes[v0:v0 + 16384]
+        sw = np.repeat(np.repeat(scale[v0 // 128:(v0 + c.shape[0]) // 128], 128, 0), 128, 1)
+        dw = (ref.e4m3_decode(c) * sw).astype(np.float32).astype(np.float64)
+        exact, mag = dx @ dw.T, np.abs(dx) @ np.abs(dw).T
+        g = got[:, v0:v0 + c.shape[0]].astype(np.float64)
+        half_ulp = np.ldexp(1.0, np.frexp(np.abs(exact).astype(np.float32))[1] - 9)   # bf16: 8 significant bits
+        excess = (np.abs(g - exact) - half_ulp) / np.maximum(mag, 1e-30)
+        worst = max(worst, float(excess.max()))
+        same += int((g == ref.bf16_round(exact.astype(np.float32))).sum())
+        total += g.size
+    assert worst <= 2.0 ** -14, f"worst (|err| - half ulp) / sum|xw| = 2^{np.log2(worst):.2f}"
+    assert same / total > 0.98, same / total
+
+
+def test_c3_512_blocks(gpu_lib):
+    """C3 (N = 32,768, prefix masks of length U{1..8}, gamma = 2): row statistics, dl and dh
+    on 512 whole blocks against the oracle.  On every row, the metrics agree with the row
+    statistics, and the size-independent properties hold."""
+    hidden, weight, markov, teacher, slots = synthetic.c3(DEV)
+    o = Objective(block_size=K, gamma=2.0)
+    m, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
+    dh, dl = head.lm_head_ce_kl_backward(saved, return_dlogits=True)
+    torch.cuda.synchronize()
+    n = hidden.shape[0]
+    rs = _np(saved.row_stats)
+    wt = _np(slots.weights).reshape(-1).astype(np.float64)
+    valid = slots.valid.cpu().numpy()
+    got = _metrics(m)
+    den = wt.sum()
+    assert got["denominator"] == pytest.approx(den, rel=1e-6)
+    assert got["ce"] == pytest.approx((wt * rs[:, 2]).sum() / den, rel=1e-5)
+    assert got["kl"] == pytest.approx((wt * rs[:, 3]).sum() / den, rel=1e-5)
+    s, tot = ref.acceptance_length_counts(rs[:, 4].reshape(-1, K), valid)
+    assert got["accept_len_sum"] == pytest.approx(s, rel=1e-5) and got["accept_len_total"] == tot
+    _assert_row_properties(rs, dl, dh, weight, slots)
+    rows = _blocks(n // K, 512)
+    w32 = _np(weight)
+    z = _head_z(hidden, w32, markov, rows)
+    u = _np(teacher[torch.as_tensor(rows, device=DEV)])
+    _, rows_ref = _oracle_rows(z, u, slots, o, rows)
+    _assert_rows(rs[rows], rows_ref)
+    w, y, _ = _slot_arrays(slots, rows)
+    dl_ref = ref.ce_kl_backward(z, u, w, y, o.ce, o.kl, dtype=np.float32).astype(np.float32)
+    del z, u
+    r_dev = torch.as_tensor(rows, device=DEV)
+    _assert_dl(_np(dl.reshape(n, -1)[r_dev]), dl_ref)
+    _assert_dh_rows(_np(dh.reshape(n, -1)[r_dev]), ref.lm_head_backward(dl_ref, w32, dtype=np.float32))
+
+
+def test_near_agreement_teacher_full_vocab(gpu_lib):
+    """The teacher is the draft's logits plus N(0, 0.5^2) noise, at full V and d (2048 C2 rows).
+    Accept rates are 0.5-0.9 and KL is about 0.1, against LSEs of 12-17, so KL's three terms
+    cancel.  Every metric agrees with the oracle to 1e-4."""
+    hidden, weight, markov, _, slots = synthetic.c2(DEV)
+    n = 2048
+    hidden, markov = hidden[:n], markov[:n]
+    slots = synthetic.Slots(slots.weights[: n // K], slots.target_ids[: n // K], slots.valid[: n // K])
+    g = torch.Generator(device=DEV).manual_seed(4242)
+    z = head.lm_head_linear(hidden, weight, markov)
+    teacher = (z.float() + 0.5 * torch.randn(z.shape, generator=g, device=DEV)).bfloat16()
+    del z
+    m_ref, rows_ref = _check_head(hidden, weight, markov, teacher, _np(teacher), slots, Objective(block_size=K),
+                                  dl_blocks=32)
+    assert 0.5 < float(np.mean(rows_ref["accept_rate"])) < 0.95
+    assert float(np.mean(rows_ref["kl"])) < 0.5
+    assert m_ref["accept_len"] > 2.0
+
+
+def _assert_row_properties(rs, dl, dh, weight, slots):
+    """Size-independent properties on every row of a full-size run:
+    * CE = lse_z - z_y >= 0, KL >= 0 and 0 <= accept rate <= 1;
+    * each dl row sums to ~0 (sum p = sum t = 1 cancels the three terms) and masked rows
+      are exactly 0;
+    * dh = dl . W on every row, through a random projection r: dh r = dl (W r), to the
+      bf16 rounding of dh (2^-8 of sum |dh_j r_j|) plus 1e-5 of the largest such sum."""
+    assert np.all(rs[:, 2] >= -1e-4) and np.all(rs[:, 3] >= -1e-4)
+    assert np.all((rs[:, 4] >= 0.0) & (rs[:, 4] <= 1.0 + 1e-5))
+    d = weight.shape[1]
+    dl2, dh2 = dl.reshape(-1, dl.shape[-1]), dh.reshape(-1, d)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    r = torch.randn(d, generator=g, device=DEV)
+    wr = weight.float() @ r
+    masked = ~slots.valid.reshape(-1)
+    lhs, rhs, mag = [], [], []
+    for i in range(0, dl2.shape[0], 4096):     # fp32 copies a chunk of rows at a time
+        dlf = dl2[i:i + 4096].float()
+        row_sum = dlf.sum(-1).abs()
+        row_abs = dlf.abs().sum(-1).clamp_min(1e-30)
+        assert float((row_sum / row_abs).max()) < 1e-2, i
+        assert torch.count_nonzero(dl2[i:i + 4096][masked[i:i + 4096]]) == 0, i
+        dhf = dh2[i:i + 4096].float()
+        lhs.append(dhf @ r)
+        rhs.append(dlf @ wr)
+        mag.append(dhf.abs() @ r.abs())
+        del dlf, dhf
+    lhs, rhs, mag = torch.cat(lhs), torch.cat(rhs), torch.cat(mag)
+    err = (lhs - rhs).abs()
+    tol = 2.0 ** -8 * mag + 1e-5 * mag.max()
+    assert bool((err <= tol).all()), float((err - tol).max())

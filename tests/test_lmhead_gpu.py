@@ -2,8 +2,9 @@
 ns_lmhead_linear) against the CPU oracle.
 
 Tolerances (north star): loss, ce, kl, accept_len within 1e-4 relative of the
-fp32 objective; the label pick exact in index; dhidden max error <= 2e-2 of
-max|dh| and cosine >= 0.9999; dl within one bf16 ulp plus fp32 evaluation error.
+fp32 objective; the label pick exact in index; dhidden per row max error <= 2e-2
+of the row's max|dh| and cosine >= 0.9999; dl within one bf16 ulp plus fp32
+evaluation error.  The benchmark sizes are in test_fullsize_gpu.py.
 """
 
 import numpy as np
@@ -45,12 +46,17 @@ def _assert_dl(dl_gpu, dl_ref):
 
 
 def _assert_dh(dh_gpu, dh_ref):
-    """North-star dhidden bar: max error <= 2e-2 of max|dh| and cosine >= 0.9999,
-    the cosine taken per row (compare.py:80-89 reports row cosines)."""
+    """North-star dhidden bar, per row: the row's largest error <= 2e-2 of its largest
+    |dh| and the row cosine >= 0.9999 (compare.py:80-89 reports row cosines)."""
     sim = ref.similarity(dh_gpu, dh_ref)
     assert sim["zero_rows_nonzero"] == 0, sim   # masked slots give exactly zero rows
     assert sim["cosine_min"] >= 0.9999, sim
-    assert sim["max_abs"] <= 2e-2 * np.abs(dh_ref).max(), sim
+    g = np.asarray(dh_gpu, dtype=np.float64).reshape(-1, dh_ref.shape[-1])
+    w = np.asarray(dh_ref, dtype=np.float64).reshape(g.shape)
+    rmax = np.abs(w).max(-1)
+    live = rmax > 0
+    err = np.abs(g - w).max(-1)[live] / rmax[live]
+    assert err.size == 0 or err.max() <= 2e-2, float(err.max())
 
 
 def _oracle_head(hidden, weight, markov, teacher, slots, o, rows=None, dtype=np.float64):
@@ -151,73 +157,3 @@ def test_deterministic(gpu_lib):
     assert torch.equal(dl1, dl2) and torch.equal(dh1, dh2)
     for f in FIELDS:
         assert torch.equal(getattr(m1, f), getattr(m2, f))
-
-
-def _check_large(hidden, weight, markov, teacher, slots, o, blocks):
-    m, saved, dh, dl = _run(hidden, weight, markov, teacher, slots, o)
-    rs = _np(saved.row_stats)
-    wt = _np(slots.weights).reshape(-1).astype(np.float64)
-    valid = slots.valid.cpu().numpy()
-    got = _metrics(m)
-    den = wt.sum()
-    assert got["denominator"] == pytest.approx(den, rel=1e-6)
-    assert got["ce"] == pytest.approx((wt * rs[:, 2]).sum() / den, rel=1e-5)
-    assert got["kl"] == pytest.approx((wt * rs[:, 3]).sum() / den, rel=1e-5)
-    s, tot = ref.acceptance_length_counts(rs[:, 4].reshape(-1, 8), valid)
-    assert got["accept_len_sum"] == pytest.approx(s, rel=1e-5) and got["accept_len_total"] == tot
-    k = 8
-    rows = np.concatenate([np.arange(b * k, b * k + k) for b in blocks])
-    z, m_ref, r, dl_ref, dh_ref = _oracle_head(hidden, weight, markov, teacher, slots, o, rows=rows,
-                                               dtype=np.float32)
-    np.testing.assert_allclose(rs[rows, 0], r["lse_z"], rtol=5e-6, atol=1e-4)
-    np.testing.assert_allclose(rs[rows, 2], r["ce"], rtol=2e-5, atol=1e-4)
-    np.testing.assert_allclose(rs[rows, 3], r["kl"], rtol=1e-4, atol=1e-4)
-    np.testing.assert_allclose(rs[rows, 4], r["accept_rate"], atol=2e-5)
-    _assert_dl(_np(dl.reshape(-1, dl.shape[-1])[rows]), dl_ref)
-    _assert_dh(_np(dh.reshape(-1, dh.shape[-1])[rows]), dh_ref)
-    _assert_row_properties(rs, dl, dh, weight, slots)
-
-
-def _assert_row_properties(rs, dl, dh, weight, slots):
-    """Size-independent properties on every row of a full-size run:
-    * CE = lse_z - z_y >= 0, KL >= 0 and 0 <= accept rate <= 1;
-    * each dl row sums to ~0 (sum p = sum t = 1 cancels the three terms) and masked rows
-      are exactly 0;
-    * dh = dl . W on every row, through a random projection r: dh r = dl (W r), to the
-      bf16 rounding of dh (2^-8 of sum |dh_j r_j|) plus 1e-5 of the largest such sum."""
-    assert np.all(rs[:, 2] >= -1e-4) and np.all(rs[:, 3] >= -1e-4)
-    assert np.all((rs[:, 4] >= 0.0) & (rs[:, 4] <= 1.0 + 1e-5))
-    d = weight.shape[1]
-    dl2, dh2 = dl.reshape(-1, dl.shape[-1]), dh.reshape(-1, d)
-    g = torch.Generator(device=DEV).manual_seed(7)
-    r = torch.randn(d, generator=g, device=DEV)
-    wr = weight.float() @ r
-    masked = ~slots.valid.reshape(-1)
-    lhs, rhs, mag = [], [], []
-    for i in range(0, dl2.shape[0], 4096):     # fp32 copies a chunk of rows at a time
-        dlf = dl2[i:i + 4096].float()
-        row_sum = dlf.sum(-1).abs()
-        row_abs = dlf.abs().sum(-1).clamp_min(1e-30)
-        assert float((row_sum / row_abs).max()) < 1e-2, i
-        assert torch.count_nonzero(dl2[i:i + 4096][masked[i:i + 4096]]) == 0, i
-        dhf = dh2[i:i + 4096].float()
-        lhs.append(dhf @ r)
-        rhs.append(dlf @ wr)
-        mag.append(dhf.abs() @ r.abs())
-        del dlf, dhf
-    lhs, rhs, mag = torch.cat(lhs), torch.cat(rhs), torch.cat(mag)
-    err = (lhs - rhs).abs()
-    tol = 2.0 ** -8 * mag + 1e-5 * mag.max()
-    assert bool((err <= tol).all()), float((err - tol).max())
-
-
-def test_c2_full_size(gpu_lib):
-    """C2: N = 4096, d = 5120, V = 248,320 (whole-block oracle + metric consistency)."""
-    hidden, weight, markov, teacher, slots = synthetic.c2(DEV)
-    _check_large(hidden, weight, markov, teacher, slots, Objective(block_size=8), blocks=(0, 301))
-
-
-def test_c3_full_size(gpu_lib):
-    """C3: N = 32,768, ragged prefix masks, gamma = 2."""
-    hidden, weight, markov, teacher, slots = synthetic.c3(DEV)
-    _check_large(hidden, weight, markov, teacher, slots, Objective(block_size=8, gamma=2.0), blocks=(5, 4000))
