@@ -140,6 +140,20 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
                         float inv_acc, void* dl, int64_t ldd, float* row_stats, float* metrics, void* workspace,
                         size_t workspace_bytes, ns_stream_t stream);
 
+/* ns_lmhead_ce_kl_fwd without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Its scratch is a static device array of 16 MiB per GPU,
+ * held until the process ends (the fused forward needs about 2.6 MB at N = 4096 and
+ * 10.6 MB at N = 32768 for V = 248,320); larger n * V is refused with NS_EWORKSPACE.
+ * Nothing in the scratch has to start at zero.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (two streams, two threads) race; serialise them. */
+int ns_lmhead_ce_kl_fwd_noalloc(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                                int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
+                                const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,
+                                const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k, float c_ce,
+                                float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats, float* metrics,
+                                ns_stream_t stream);
+
 /* The same forward with the Markov head in factored form (train.py:276-279):
  * z = hidden . weight^T + w1[prev] . w2^T, formed as one GEMM with K = d + r
  * ([hidden | w1[prev]] . [weight | w2]^T), so no [N, V] Markov tensor is read.

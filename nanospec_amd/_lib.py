@@ -67,6 +67,11 @@ SIGNATURES = {
          _P, _I64, _P, _P, _P, _SZ, _P],
         _I,
     ),
+    "ns_lmhead_ce_kl_fwd_noalloc": (
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _TEACH, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F,
+         _P, _I64, _P, _P, _P],
+        _I,
+    ),
     "ns_lmhead_markov_ce_kl_fwd": (
         [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I, _I64, _TEACH, _P, _P, _P, _I64, _I64, _I64,
          _I64, _F, _F, _F, _P, _I64, _P, _P, _P, _SZ, _P],

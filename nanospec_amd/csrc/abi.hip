@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/nanospec_hip.h"
 #include "ns_internal.h"
 
@@ -228,6 +230,62 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
   return lmhead_fwd_checked(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, teacher_args,
                             labels, weights, valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics,
                             workspace, workspace_bytes, stream, "ns_lmhead_ce_kl_fwd");
+}
+
+}  // extern "C"
+
+namespace {
+
+// Scratch of ns_lmhead_ce_kl_fwd_noalloc: one array per GPU for the life of the process.
+// In host code `scratch` names a host-side stand-in, never the device memory: kernels get
+// the address hipGetSymbolAddress returns for the current device (kept per device below).
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device.
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(NS_EINVAL, "device %d beyond the %d devices supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+      return hip_status(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ns_lmhead_ce_kl_fwd_noalloc(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
+                                int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
+                                const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,
+                                const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k, float c_ce,
+                                float c_kl, float inv_acc, void* dl, int64_t ldd, float* row_stats, float* metrics,
+                                ns_stream_t stream) {
+  const size_t need = n > 0 && v > 0 ? ns::lmhead_workspace_bytes(n, v, d) : 0;
+  if (need > kNoAllocScratchBytes)
+    return fail(NS_EWORKSPACE,
+                "ns_lmhead_ce_kl_fwd_noalloc: n = %lld, v = %lld need %zu bytes of scratch; its static scratch "
+                "holds %zu (use ns_lmhead_ce_kl_fwd with a workspace)",
+                (long long)n, (long long)v, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (n > 0) {
+    const int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+  }
+  return lmhead_fwd_checked(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, teacher_args,
+                            labels, weights, valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics, ws,
+                            kNoAllocScratchBytes, stream, "ns_lmhead_ce_kl_fwd_noalloc");
 }
 
 int ns_lmhead_markov_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const int64_t* prev,
