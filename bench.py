@@ -38,6 +38,8 @@ def parse():
                    help="one workload alone; default: C2 (the headline) and then C1 and C4 as secondary lines")
     p.add_argument("--no-secondary", action="store_true", help="default run: C2 only")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--markov-skew", type=float, default=0.0,
+                   help="c2x: fraction of rows sharing one previous-token id (the W1 scatter's worst case)")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU-baseline sample (0: default)")
     p.add_argument("--pmc-driver", action="store_true",
                    help="short run for one rocprofv3 --pmc pass: a 1 GiB calibration kernel, then two steps")
@@ -565,6 +567,11 @@ def workload_c2x(device, args):
     norm_w = torch.ones(d, dtype=torch.bfloat16, device=device)
     norm_g = torch.zeros_like(norm_w)
     prev, w1, w2 = synthetic.markov_factors(n, v, r, 2002, device)
+    if args.markov_skew > 0:
+        # dropped anchor blocks give every slot the block's first id (dspark.py:120-127): a
+        # fraction of the rows, spread over the batch, share one previous-token id
+        hot = torch.randperm(n, generator=torch.Generator(device=device).manual_seed(4002), device=device)
+        prev[hot[: int(args.markov_skew * n)]] = int(prev[0])
     mk = head.MarkovFactors(prev, w1, w2)
     w1_grad = torch.zeros_like(w1)
     w2_grad = torch.zeros_like(w2)
@@ -623,8 +630,8 @@ def workload_c2x(device, args):
     config = {"workload": "C2X: C2 with final_norm around the head, the factored Markov head (r=256) fused "
                           "as a second K segment, and the pooled tail; fwd, dl + dx + final_norm / markov_w1 / "
                           "markov_w2 grads bwd, gradient factor applied",
-              "N": n, "d": d, "V": v, "K": 8, "r": r, "gamma": 4.0, "global_batch": n, "seq_len": None,
-              "parallelism": "single GPU"}
+              "N": n, "d": d, "V": v, "K": 8, "r": r, "gamma": 4.0, "markov_skew": args.markov_skew,
+              "global_batch": n, "seq_len": None, "parallelism": "single GPU"}
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d + 6.0 * v * r,
                 kernel_bytes=kernel_bytes, kernel_flops=kernel_flops, kernel_fp8_flops={},
                 cpu_baseline=cpu_baseline, config=config, dtype="bf16", per_slot_fp8_flops=None,

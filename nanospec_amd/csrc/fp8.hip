@@ -83,44 +83,50 @@ struct Fp8Params {
   RowPart* part;           // [N][splits] (max, sum-exp) of the stored bf16 values, or null
 };
 
-// Workgroup tile: 256 vocab rows (two weight-scale row blocks) x 128 tokens, 4 waves as
-// 2 (vocab) x 2 (tokens), each 128 x 64 = 4 x 2 blocks of 32 x 32.  K advances one
-// 128-entry quantisation block per stage; stages live in a 3-deep LDS ring so the fills
-// of stage t + 2 can be issued anywhere in stage t.
+// Workgroup tile: 256 vocab rows (two weight-scale row blocks) x 256 tokens on 8 waves, two
+// per SIMD, as 2 (vocab) x 4 (tokens), each 128 x 64 = 4 x 2 blocks of 32 x 32 with its
+// accumulator in 128 VGPRs.  K advances one 128-entry quantisation block per stage; a stage
+// is 32 KB of weight codes plus 32 KB of activation codes, in a 2-deep LDS ring.  Against a
+// 256 x 128 tile on 4 waves this moves a third fewer fill bytes per MFMA, and a wave that
+// stalls on a fill or on its fold leaves the SIMD's matrix core to the other wave.
 constexpr int FM = 256;
-constexpr int FN = 128;
-constexpr int kThreads = 256;
+constexpr int FN = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kAStage = FM * kQBlock;        // 32 KB of weight codes
-constexpr int kBStage = FN * kQBlock;        // 16 KB of activation codes
+constexpr int kBStage = FN * kQBlock;        // 32 KB of activation codes
 constexpr int kStage = kAStage + kBStage;
-constexpr int kRing = 3;
-constexpr int kRingLds = kRing * kStage;     // 144 KB
+constexpr int kRing = 2;
+constexpr int kRingLds = kRing * kStage;     // 128 KB
 constexpr int kLseOff = kRingLds;            // [FN][2] fp32 running (max, sum-exp) per token
 constexpr int kFp8Lds = kLseOff + FN * 8;
 constexpr int kOutRow = FM * 2 + 16;         // bf16 output row in the LDS transpose (+16 B)
-static_assert(FN * kOutRow <= kRingLds, "output transpose fits in the ring");
+constexpr int kOutTokens = 128;              // tokens per output pass (two passes per tile)
+static_assert(kOutTokens * kOutRow <= kRingLds, "output transpose fits in the ring");
+static_assert(kFp8Lds <= 160 * 1024, "fp8 head LDS");
 
-// s_waitcnt vmcnt(12) lgkmcnt(0) (expcnt not waited): gfx9 encoding, vmcnt[3:0] in bits
+// s_waitcnt vmcnt(0) lgkmcnt(0) (expcnt not waited): gfx9 encoding, vmcnt[3:0] in bits
 // 3:0, expcnt in 6:4, lgkmcnt in 11:8, vmcnt[5:4] in 15:14.
-constexpr int kWaitStage = 12 | (7 << 4);
+constexpr int kWaitAll = 0 | (7 << 4);
+// vmcnt(8): everything but the last 8 vector-memory operations (the next stage's fills)
+constexpr int kWaitPrologue = 8 | (7 << 4) | (15 << 8);
 
 __device__ __forceinline__ u32x4_t rd16(const lds_t* base, int row, int chunk) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(base + lds_off(row, chunk));
 }
 
-__device__ __forceinline__ i32x8_t join(const u32x4_t& lo, const u32x4_t& hi) {
-  i32x8_t r;
-  r[0] = (int)lo[0]; r[1] = (int)lo[1]; r[2] = (int)lo[2]; r[3] = (int)lo[3];
-  r[4] = (int)hi[0]; r[5] = (int)hi[1]; r[6] = (int)hi[2]; r[7] = (int)hi[3];
-  return r;
+// One lane's 32-byte fp8 MFMA operand: logical chunks c0 and c0 + 1 of `row` (c0 even),
+// read straight into the two halves of one 8-register vector.
+__device__ __forceinline__ i32x8_t rd32(const lds_t* base, int row, int c0) {
+  const u32x4_t lo = rd16(base, row, c0), hi = rd16(base, row, c0 + 1);
+  return __builtin_bit_cast(i32x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // One fp8 MFMA block product: 32 x 32 outputs over 64 K-entries.  Operand lane layout:
 // lane r + 32 kh holds row r, K entries 32 kh .. 32 kh + 31 of the 64 (two 16-byte
 // chunks); unit e8m0 scales (127).
-__device__ __forceinline__ f32x16_t mfma_f8(const u32x4_t (&a)[2], const u32x4_t (&b)[2], const f32x16_t& c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(join(a[0], a[1]), join(b[0], b[1]), c, 0, 0, 0, 127, 0,
-                                                          127);
+__device__ __forceinline__ f32x16_t mfma_f8(const i32x8_t& a, const i32x8_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
 // Reductions over the 16 lanes of a DPP row with every lane receiving the result:
@@ -145,7 +151,27 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x + dpp_mov<0x140>(x);
 }
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// acc[e0 .. e0 + 8) += c * part[e0 .. e0 + 8).  The empty asm statements pin each sum where
+// it is formed: the optimiser otherwise sinks these FMAs to the end of the stage, which
+// keeps every 32 x 32 block's partial alive at once.
+__device__ __forceinline__ void fold8(f32x16_t& acc, const f32x16_t& part, float c, int e0) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float x = __builtin_fmaf(c, part[e0 + e], acc[e0 + e]);
+    asm volatile("" : "+v"(x));
+    acc[e0 + e] = x;
+  }
+}
+
+template <int WAITCNT>
+__device__ __forceinline__ void wait_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(WAITCNT);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fp8_head_kernel(Fp8Params p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_t* lds = (lds_t*)lds_raw;
@@ -155,22 +181,21 @@ void fp8_head_kernel(Fp8Params p) {
   const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv >> 2, wn = wv & 3;
   const int lane = tid & 63, r = lane & 31, kh = lane >> 5;
   const int KB = (int)(p.d / kQBlock);
   const int64_t t0 = (int64_t)tile_t * FN;
   const int nvb = (int)(p.v / kQBlock);
-  auto buf = [&](int t) -> lds_t* { return lds + (t % kRing) * kStage; };
-  auto clampk = [&](int t) -> int64_t { return (int64_t)(t < KB - 1 ? t : KB - 1) * kQBlock; };
+  auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * kStage; };
 
-  DmaTile<FN> tb;
+  DmaTile<FN, kWaves> tb;
   tb.init(p.d, t0, p.n, wv);
   const char* pb = reinterpret_cast<const char*>(p.qx + t0 * p.d);
-  const float* xsrow[2];
+  uint32_t xsoff[2];   // this lane's two tokens' rows of xs (element offsets; N * d/128 < 2^31)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t t = t0 + wn * 64 + j * 32 + r;
-    xsrow[j] = p.xs + (t < p.n ? t : p.n - 1) * KB;
+    xsoff[j] = (uint32_t)((t < p.n ? t : p.n - 1) * KB);
   }
   lds_f32* lse_st = reinterpret_cast<lds_f32*>(lds + kLseOff);
   if (p.part && tid < FN) {   // first read after the first tile's barriers
@@ -180,7 +205,7 @@ void fp8_head_kernel(Fp8Params p) {
 
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int64_t v0 = (int64_t)vt * FM;
-    DmaTile<FM> ta;
+    DmaTile<FM, kWaves> ta;
     ta.init(p.ldw, v0, p.v, wv);
     const char* pa = reinterpret_cast<const char*>(p.wq + v0 * p.ldw);
     int vb = (int)(v0 / kQBlock) + wm;   // this wave's weight-scale row block
@@ -195,104 +220,88 @@ void fp8_head_kernel(Fp8Params p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[q][j][e] = 0.f;
 
-    // prologue: stages 0 and 1 in flight, stage 0's scales, then stage 0's fragments
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ta.issue(pa, buf(0), wv, i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tb.issue(pb, buf(0) + kAStage, wv, i);
-    {
-      const int64_t k1 = clampk(1);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ta.issue(pa + k1, buf(1), wv, i);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) tb.issue(pb + k1, buf(1) + kAStage, wv, i);
-    }
+    // prologue: stage 0's scales, then the fills of stages 0 and 1; wait for stage 0 only
+    // (vector-memory operations complete in order)
     float c_cur[2], c_prev[2] = {0.f, 0.f}, xn[2], wnx;
     {
       const float w0 = wsrow[0];
-      c_cur[0] = xsrow[0][0] * w0;
-      c_cur[1] = xsrow[1][0] * w0;
+      c_cur[0] = p.xs[xsoff[0]] * w0;
+      c_cur[1] = p.xs[xsoff[1]] * w0;
     }
-    fill_barrier();
-    u32x4_t a[2][2][2];      // [q parity][kk][chunk half]
-    u32x4_t b[2][2][2][2];   // [stage parity][j][kk][chunk half]
-    f32x16_t part[2][2];     // [q parity][j]
+    const int64_t k1 = KB > 1 ? kQBlock : 0;
+#pragma unroll
+    for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa, buf(0), wv, i);
+#pragma unroll
+    for (int i = 0; i < DmaTile<FN, kWaves>::NI; ++i) tb.issue(pb, buf(0) + kAStage, wv, i);
+#pragma unroll
+    for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa + k1, buf(1), wv, i);
+#pragma unroll
+    for (int i = 0; i < DmaTile<FN, kWaves>::NI; ++i) tb.issue(pb + k1, buf(1) + kAStage, wv, i);
+    wait_barrier<kWaitPrologue>();
+
+    i32x8_t a[2];            // [kk]: block row q's A fragments, reloaded after their last use
+    i32x8_t b[2][2];         // [j][kk]
+    f32x16_t part[2];        // [j]: the pair of MFMAs of one 32 x 32 block over 128 K
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+      for (int kk = 0; kk < 2; ++kk) b[j][kk] = rd32(buf(0) + kAStage, wn * 64 + j * 32 + r, kk * 4 + kh * 2);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          b[0][j][kk][h] = rd16(buf(0) + kAStage, wn * 64 + j * 32 + r, kk * 4 + kh * 2 + h);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) a[0][kk][h] = rd16(buf(0), wm * 128 + r, kk * 4 + kh * 2 + h);
+    for (int kk = 0; kk < 2; ++kk) a[kk] = rd32(buf(0), wm * 128 + r, kk * 4 + kh * 2);
 
-    // one stage; the parity SP of the B fragment buffers is a compile-time constant so
-    // the fragment arrays stay in registers
-    auto stage = [&](int t, auto spc) {
-      constexpr int sp = decltype(spc)::value;
+    for (int t = 0; t < KB; ++t) {
       const lds_t* cb = buf(t);
       const lds_t* nb = buf(t + 1);
-      lds_t* db = buf(t + 2);
-      const int64_t k2 = clampk(t + 2);
-      const int kn = t + 1 < KB ? t + 1 : KB - 1;
-      // 16 MFMA slots: s = 4 q + 2 kk + j; between them, one or more of the stage's other
-      // operations (sched_barrier keeps the order)
+      lds_t* db = buf(t);              // stage t + 2 lands where stage t was
+      const int64_t k2 = (int64_t)(t + 2) * kQBlock;
+      const bool more = t + 1 < KB, fill2 = t + 2 < KB;
+      const int kn = more ? t + 1 : t;
+      // 16 MFMA slots s = 4 q + 2 j + kk; the pair (q, j) accumulates over the stage's two
+      // 64-K halves, and each pair is folded into the accumulator with the block scale two
+      // slots after it completes, 8 elements per slot (sched_barrier keeps the order)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int s = 4 * q + 2 * kk + j;
-            part[q & 1][j] = mfma_f8(a[q & 1][kk], b[sp][j][kk], kk == 0 ? f32x16_t{} : part[q & 1][j]);
+          for (int kk = 0; kk < 2; ++kk) {
+            const int s = 4 * q + 2 * j + kk;
+            part[j] = mfma_f8(a[kk], b[j][kk], kk == 0 ? f32x16_t{} : part[j]);
+            asm volatile("" : "+v"(part[j]));   // keep the MFMAs in program order
             __builtin_amdgcn_sched_barrier(0);
             if (s == 0) {   // next stage's scales (complete by this stage's barrier)
-              xn[0] = xsrow[0][kn];
-              xn[1] = xsrow[1][kn];
+              xn[0] = p.xs[xsoff[0] + kn];
+              xn[1] = p.xs[xsoff[1] + kn];
               wnx = wsrow[kn];
             }
-            if (s < 8) ta.issue(pa + k2, db, wv, s);
-            else if (s < 12) tb.issue(pb + k2, db + kAStage, wv, s - 8);
-            if (q < 3) {     // block row q + 1's A fragments, one chunk per slot
-              const int p4 = s & 3;
-              a[(q + 1) & 1][p4 >> 1][p4 & 1] =
-                  rd16(cb, wm * 128 + (q + 1) * 32 + r, (p4 >> 1) * 4 + kh * 2 + (p4 & 1));
+            if (j == 1) {   // block (q, 0) completed two slots ago
+              fold8(acc[q][0], part[0], c_cur[0], kk * 8);
+            } else if (q > 0) {   // block (q - 1, 1)
+              fold8(acc[q - 1][1], part[1], c_cur[1], kk * 8);
+            } else if (t > 0) {   // the previous stage's block (3, 1)
+              fold8(acc[3][1], part[1], c_prev[1], kk * 8);
             }
-            // fold block (q - 1, j') into the accumulator, 8 elements per slot; slots of
-            // q = 0 fold the previous stage's block row 3
-            {
-              const int jj = (s & 3) >> 1, e0 = (s & 1) * 8;
-              if (q > 0) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                  acc[q - 1][jj][e0 + e] = __builtin_fmaf(c_cur[jj], part[(q - 1) & 1][jj][e0 + e], acc[q - 1][jj][e0 + e]);
-              } else if (t > 0) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                  acc[3][jj][e0 + e] = __builtin_fmaf(c_prev[jj], part[1][jj][e0 + e], acc[3][jj][e0 + e]);
-              }
+            // block row q + 1's A fragment kk, after its last use by block (q, 1)
+            if (q < 3 && j == 1) a[kk] = rd32(cb, wm * 128 + (q + 1) * 32 + r, kk * 4 + kh * 2);
+            if (s == 11) {  // stage t + 1 landed everywhere, every wave done reading stage t
+              wait_barrier<kWaitAll>();
             }
-            if (s == 11) {   // stage t + 1 landed everywhere; buffer t free after this
-              asm volatile("" ::: "memory");
-              __builtin_amdgcn_s_waitcnt(kWaitStage);
-              __builtin_amdgcn_s_barrier();
-              asm volatile("" ::: "memory");
-            }
-            if (q == 3) {    // stage t + 1's fragments: B (8 chunks) and A row 0 (4)
-              const int u = s - 12;
+            if (q == 3) {
+              const int u = s - 12;   // 0..3
+              // stage t + 2's fills into stage t's buffer, two per slot
+              if (fill2) {
 #pragma unroll
-              for (int m = 0; m < 3; ++m) {
-                const int o = 3 * u + m;   // 0..11
-                if (o < 8) {
-                  const int j2 = o >> 2, kk2 = (o >> 1) & 1, h2 = o & 1;
-                  b[sp ^ 1][j2][kk2][h2] = rd16(nb + kAStage, wn * 64 + j2 * 32 + r, kk2 * 4 + kh * 2 + h2);
-                } else {
-                  const int o4 = o - 8;
-                  a[0][o4 >> 1][o4 & 1] = rd16(nb, wm * 128 + r, (o4 >> 1) * 4 + kh * 2 + (o4 & 1));
+                for (int m = 0; m < 2; ++m) {
+                  const int o = 2 * u + m;   // 0..7
+                  if (o < DmaTile<FM, kWaves>::NI) ta.issue(pa + k2, db, wv, o);
+                  else tb.issue(pb + k2, db + kAStage, wv, o - DmaTile<FM, kWaves>::NI);
                 }
+              }
+              // stage t + 1's fragments, each right after its last use in this stage: B (j, kk)
+              // in its own slot, A row 0 in the slots of block (3, 1)
+              if (more) {
+                b[j][kk] = rd32(nb + kAStage, wn * 64 + j * 32 + r, kk * 4 + kh * 2);
+                if (j == 1) a[kk] = rd32(nb, wm * 128 + r, kk * 4 + kh * 2);
               }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -303,82 +312,83 @@ void fp8_head_kernel(Fp8Params p) {
       c_prev[1] = c_cur[1];
       c_cur[0] = xn[0] * wnx;
       c_cur[1] = xn[1] * wnx;
-    };
-    for (int t = 0; t < KB; t += 2) {
-      stage(t, std::integral_constant<int, 0>{});
-      if (t + 1 < KB) stage(t + 1, std::integral_constant<int, 1>{});
     }
-    // the last stage's block row 3
+    // the last stage's block (3, 1)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[3][j][e] = __builtin_fmaf(c_prev[j], part[1][j][e], acc[3][j][e]);
-    fill_barrier();   // no fill in flight, every wave done with the ring
+    for (int e = 0; e < 16; ++e) acc[3][1][e] = __builtin_fmaf(c_prev[1], part[1][e], acc[3][1][e]);
+    wait_barrier<kWaitAll>();   // no fill in flight, every wave done with the ring
 
-    // bf16 tile transposed through LDS, then whole 16-byte chunks of output rows
+    // bf16 tile transposed through LDS in two passes of 128 tokens, then whole 16-byte
+    // chunks of output rows
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int half = 0; half < 2; ++half) {
+      if ((wn >> 1) == half) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int tl = wn * 64 + j * 32 + r;
-          const int vl = wm * 128 + q * 32 + 8 * g + 4 * kh;
-          const u32x2_t y = {pack_bf16x2(acc[q][j][4 * g], acc[q][j][4 * g + 1]),
-                             pack_bf16x2(acc[q][j][4 * g + 2], acc[q][j][4 * g + 3])};
-          *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + tl * kOutRow + vl * 2) = y;
-        }
-    __syncthreads();
-    // 16 lanes per output row (one DPP row), each taking 16-byte chunks c and c + 16
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int tl = (wn & 1) * 64 + j * 32 + r;
+              const int vl = wm * 128 + q * 32 + 8 * g + 4 * kh;
+              const u32x2_t y = {pack_bf16x2(acc[q][j][4 * g], acc[q][j][4 * g + 1]),
+                                 pack_bf16x2(acc[q][j][4 * g + 2], acc[q][j][4 * g + 3])};
+              *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + tl * kOutRow + vl * 2) = y;
+            }
+      }
+      __syncthreads();
+      // 16 lanes per output row (one DPP row), each taking 16-byte chunks c and c + 16
 #pragma unroll 2
-    for (int i = 0; i < FN * (FM / 16) / kThreads; ++i) {
-      const int ci = i * kThreads + tid;
-      const int row = ci >> 4, c = ci & 15;
-      const int64_t t = t0 + row;
-      float f[2][8];
-      bool in[2];
+      for (int i = 0; i < kOutTokens * (FM / 16) / kThreads; ++i) {
+        const int ci = i * kThreads + tid;
+        const int row = ci >> 4, c = ci & 15;
+        const int tk = half * kOutTokens + row;   // token within the tile
+        const int64_t t = t0 + tk;
+        float f[2][8];
+        bool in[2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int chunk = c + 16 * h;
-        const int64_t v = v0 + chunk * 8;
-        in[h] = t < p.n && v < p.v;
-        const u32x4_t x =
-            *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + row * kOutRow + chunk * 16);
-        if (in[h]) *reinterpret_cast<uint4*>(p.out + t * p.ldo + v) = make_uint4(x[0], x[1], x[2], x[3]);
+        for (int h = 0; h < 2; ++h) {
+          const int chunk = c + 16 * h;
+          const int64_t v = v0 + chunk * 8;
+          in[h] = t < p.n && v < p.v;
+          const u32x4_t x =
+              *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + row * kOutRow + chunk * 16);
+          if (in[h]) *reinterpret_cast<uint4*>(p.out + t * p.ldo + v) = make_uint4(x[0], x[1], x[2], x[3]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f[h][2 * e] = bf16_lo(x[e]);
-          f[h][2 * e + 1] = bf16_hi(x[e]);
+          for (int e = 0; e < 4; ++e) {
+            f[h][2 * e] = bf16_lo(x[e]);
+            f[h][2 * e + 1] = bf16_hi(x[e]);
+          }
+        }
+        if (p.part) {
+          // log-sum-exp of the stored bf16 row over this tile: the row maximum first, then
+          // one exponential per entry against it, then the sum
+          float m = kNegBig;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            if (in[h]) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) m = fmaxf(m, f[h][e]);
+            }
+          m = row16_max(m);
+          const float ml = m * kLog2e;
+          float sum = 0.f;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            if (in[h]) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) sum += fast_exp2(__builtin_fmaf(f[h][e], kLog2e, -ml));
+            }
+          sum = row16_sum(sum);
+          if (c == 0) {
+            const LseState r2 = lse_merge(LseState{lse_st[2 * tk], lse_st[2 * tk + 1]}, LseState{m, sum});
+            lse_st[2 * tk] = r2.m;
+            lse_st[2 * tk + 1] = r2.s;
+          }
         }
       }
-      if (p.part) {
-        // log-sum-exp of the stored bf16 row over this tile: the row maximum first, then
-        // one exponential per entry against it, then the sum
-        float m = kNegBig;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          if (in[h]) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) m = fmaxf(m, f[h][e]);
-          }
-        m = row16_max(m);
-        const float ml = m * kLog2e;
-        float sum = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          if (in[h]) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sum += fast_exp2(__builtin_fmaf(f[h][e], kLog2e, -ml));
-          }
-        sum = row16_sum(sum);
-        if (c == 0) {
-          const LseState r2 = lse_merge(LseState{lse_st[2 * row], lse_st[2 * row + 1]}, LseState{m, sum});
-          lse_st[2 * row] = r2.m;
-          lse_st[2 * row + 1] = r2.s;
-        }
-      }
+      __syncthreads();
     }
-    __syncthreads();
   }
   if (p.part && tid < FN && t0 + tid < p.n) {
     RowPart rp;

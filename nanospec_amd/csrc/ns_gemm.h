@@ -37,15 +37,17 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t voff, lds_t* ds
                                            voff, 0, 0, 0);
 }
 
-// A ROWS-row operand tile (128-byte rows) fetched straight into LDS (dma16).  Each of the 4 waves issues NI = ROWS / 32 instructions per
-// stage; instruction i of wave wv fills the 1 KB LDS block wv * NI + i, i.e. rows
-// 8 (wv * NI + i) .. +8.  Lane l writes the block's 16-byte slot l, which is physical
-// chunk l % 8 of row 8 (wv * NI + i) + l / 8; the lane therefore fetches the logical
-// chunk (l % 8) ^ swz(row), so the tile lands in the swizzled lds_off layout.  Rows at or
-// past rmax re-read row rmax - 1 (their results are discarded by the caller).
-template <int ROWS>
+// A ROWS-row operand tile (128-byte rows) fetched straight into LDS (dma16).  Each of the
+// WAVES waves issues NI = ROWS / (8 WAVES) instructions per stage; instruction i of wave wv
+// fills the 1 KB LDS block wv * NI + i, i.e. rows 8 (wv * NI + i) .. +8.  Lane l writes the
+// block's 16-byte slot l, which is physical chunk l % 8 of row 8 (wv * NI + i) + l / 8; the
+// lane therefore fetches the logical chunk (l % 8) ^ swz(row), so the tile lands in the
+// swizzled lds_off layout.  Rows at or past rmax re-read row rmax - 1 (their results are
+// discarded by the caller).
+template <int ROWS, int WAVES = 4>
 struct DmaTile {
-  static constexpr int NI = ROWS / 32;
+  static constexpr int NI = ROWS / (8 * WAVES);
+  static_assert(NI * 8 * WAVES == ROWS, "whole 8-row blocks per wave");
   uint32_t off[NI];  // per-lane byte offsets from the tile's first row, stage 0
   // ld_bytes: row pitch in bytes; r0: first row; rmax: rows in the matrix
   __device__ __forceinline__ void init(int64_t ld_bytes, int64_t r0, int64_t rmax, int wv) {
