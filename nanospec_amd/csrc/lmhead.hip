@@ -4,8 +4,8 @@
 //   z^T tile = W_lm[v-tile] . hidden[t-tile]^T   (vocab on the MFMA M axis, tokens on N)
 //   pass 1 ("stats"): epilogue adds the Markov tile, reads the teacher tile and folds
 //     (max, sum-exp) of z and u plus A = sum exp(u - m_u)(u - z) into per-token running
-//     state kept in registers across the workgroup's vocab range -> RowPart partials;
-//     the lane that owns (token, label) writes z_label.
+//     state kept in LDS across the workgroup's vocab range -> RowPart partials; the lane
+//     that owns (token, label) writes z_label.
 //   merge (shared with the logits path): LSE_z, LSE_u, CE, KL per token.
 //   pass 2 ("emit"): recomputes the z tile, p = exp(z - LSE_z), t = exp(u - LSE_u),
 //     accumulates sum min(p, t) and writes dl = (w/acc)[(c_ce + c_kl) p - c_kl t - c_ce e_y]
@@ -15,9 +15,13 @@
 //
 // Layout choices (MI355X): one 256-thread workgroup per CU (4 waves, 2 x 2, each a
 // 128 x 128 accumulator tile = 256 AGPRs/lane), 256 x 256 x 64 LDS stages double
-// buffered with an XOR swizzle on 16-byte chunks, persistent workgroups that walk a
-// contiguous vocab range with per-token running statistics, and a workgroup -> tile map
-// that puts the workgroups sharing a W stream on the same XCD (shared L2).
+// buffered with an XOR swizzle on 16-byte chunks, an epilogue that works on the
+// accumulators in place while the tile's Markov and teacher rows come into the freed
+// stage buffers, persistent workgroups that walk a contiguous vocab range with per-token
+// running statistics, and a workgroup -> tile map that puts the workgroups sharing a W
+// stream on the same XCD (shared L2).
+#include <type_traits>
+
 #include "ns_gemm.h"
 #include "ns_internal.h"
 #include "ns_profile.h"
@@ -33,9 +37,6 @@ constexpr int BK = 64;           // K per LDS stage
 constexpr int kThreads = 256;    // 4 waves as 2 (M) x 2 (N), 128 x 128 each
 constexpr int kStageBytes = BM * BK * 2;    // 32 KB per operand per stage
 constexpr int kGemmLds = 4 * kStageBytes;   // 2 stages x 2 operands = 128 KB
-constexpr int kZRow = BM + 4;               // padded fp32 row of the epilogue dump
-constexpr int kDumpLds = 128 * kZRow * 4;   // 128 token rows x 256 vocab fp32
-constexpr int kLdsBytes = kGemmLds > kDumpLds ? kGemmLds : kDumpLds;
 
 
 
@@ -253,8 +254,30 @@ __device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la
 }
 
 
+// Wait for this wave's LDS operations only, then a workgroup barrier (outstanding global
+// loads, LDS fills included, keep flying).  s_waitcnt encoding: vmcnt 63, expcnt 7,
+// lgkmcnt 0.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Wait until at most N of this wave's global loads and stores are outstanding and every
+// LDS operation is done, then a workgroup barrier (vmcnt N in bits 3:0 and 15:14,
+// expcnt 7, lgkmcnt 0).
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T, both row-major with K contiguous and
-// K a multiple of BK.  Ends with a barrier (LDS free for the caller).
+// K a multiple of BK.
 //
 // Operands go global -> LDS without registers; stage t lives in LDS buffer t & 1.  A
 // stage's 64 MFMAs run one per instruction slot with the other work of the stage
@@ -267,14 +290,27 @@ __device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la
 // The barrier cannot come earlier: step 2 still reads buffer t & 1 and the step-0
 // fragment registers.  Placing it at the start of step 3 rather than after two of its
 // MFMA groups gives the next stage's first reads 8 more slots: 3.6-3.9% off each head
-// pass at C2.  Fills past the last stage re-read the last stage into the idle buffer.
+// pass at C2.
+//
+// The last stages would fill stages past the end.  With `tail.on` and KT >= 2 the slots
+// of two of those fills issue the caller's next loads instead (the epilogue's first
+// stream step, into the buffer the GEMM is done with): tail.issue(sb, 0, i, buf) in the
+// A-fill slots of stage KT - 2 (buffer KT & 1, free after that stage's barrier) and
+// tail.issue(sb, 1, i, buf) in the B-fill slots of stage KT - 1 (the same buffer); the
+// last stage issues no fills, and its step-3 barrier waits for LDS reads only, not for
+// those loads.  Returns true in that case, with the loads still in flight; otherwise
+// fills past the last stage re-read the last stage into the idle buffer and the
+// function ends with a full barrier (LDS free).
 //
 // The operand tiles come in ready-made: `ta`/`tb` hold the per-lane offsets of the
 // 256 rows of each operand from the uniform bases `pa`/`pb` (stage 0), and stage t reads
 // 128 bytes further along K each step; KT stages.
-__device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTile<256>& ta, const char* pa,
-                                              const DmaTile<256>& tb, const char* pb, int KT, lds_t* lds) {
+template <typename Tail>
+__device__ __forceinline__ bool gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTile<256>& ta, const char* pa,
+                                              const DmaTile<256>& tb, const char* pb, int KT, lds_t* lds,
+                                              const Tail& tail) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool tl = tail.on && KT >= 2;
   auto stage_k = [&](int t) -> int64_t { return (int64_t)(t < KT - 1 ? t : KT - 1) * BK * 2; };
   auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * 2 * kStageBytes; };
 #pragma unroll
@@ -290,7 +326,11 @@ __device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTi
 #pragma unroll
     for (int i = 0; i < 8; ++i) ta.issue(pa + k1, buf(1), wv, i);
   }
-  for (int t = 0; t < KT; ++t) {
+  // stage t; MODE 0: an ordinary stage, 1: stage KT - 2 and 2: stage KT - 1 with the tail
+  auto stage = [&](auto mode, int t) {
+    constexpr int M = decltype(mode)::value;
+    decltype(tail.bases()) sb{};
+    if constexpr (M != 0) sb = tail.bases();
     const lds_t* cur = buf(t);
     lds_t* nxt = buf(t + 1);
     const int64_t k1 = stage_k(t + 1), k2 = stage_k(t + 2);
@@ -300,7 +340,10 @@ __device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTi
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int cb = kk & 1;
-      if (kk == 3) fill_barrier();
+      if (kk == 3) {
+        if (M == 2) lds_barrier();
+        else fill_barrier();
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
@@ -316,35 +359,51 @@ __device__ __forceinline__ void gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTi
               f[cb ^ 1].b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
                   cur + kStageBytes + lds_off(wn * 128 + i * 32 + r, (kk + 1) * 2 + kh));
           }
-          if (kk == 0 && q >= 2) tb.issue(pb + k1, nxt + kStageBytes, wv, (q - 2) * 4 + j);
+          if (kk == 0 && q >= 2) {
+            if (M == 2) tail.issue(sb, 1, (q - 2) * 4 + j, nxt);
+            else tb.issue(pb + k1, nxt + kStageBytes, wv, (q - 2) * 4 + j);
+          }
           if (kk == 3 && q < 2) {
-            if ((j & 1) == 0)
-              f[0].a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-                  nxt + lds_off(wm * 128 + i * 32 + r, kh));
-            else
-              f[0].b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-                  nxt + kStageBytes + lds_off(wn * 128 + i * 32 + r, kh));
-            ta.issue(pa + k2, buf(t), wv, q * 4 + j);
+            if (M != 2) {
+              if ((j & 1) == 0)
+                f[0].a[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                    nxt + lds_off(wm * 128 + i * 32 + r, kh));
+              else
+                f[0].b[i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                    nxt + kStageBytes + lds_off(wn * 128 + i * 32 + r, kh));
+            }
+            if (M == 1) tail.issue(sb, 0, q * 4 + j, buf(t));
+            else if (M == 0) ta.issue(pa + k2, buf(t), wv, q * 4 + j);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
+  };
+  const int tmain = tl ? KT - 2 : KT;
+  for (int t = 0; t < tmain; ++t) stage(std::integral_constant<int, 0>(), t);
+  if (tl) {
+    stage(std::integral_constant<int, 1>(), KT - 2);
+    stage(std::integral_constant<int, 2>(), KT - 1);
   }
-  fill_barrier();
+  if (!tl) fill_barrier();
+  return tl;
 }
+
+
 
 // acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T (row-major, K contiguous, K % BK == 0);
 // rows at or past amax / bmax re-read the last row.
-__device__ __forceinline__ void gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
+template <typename Tail>
+__device__ __forceinline__ bool gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
                                         int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
-                                        int64_t b0, int64_t bmax, int64_t K, lds_t* lds) {
+                                        int64_t b0, int64_t bmax, int64_t K, lds_t* lds, const Tail& tail) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   DmaTile<256> ta, tb;
   ta.init(lda * 2, a0, amax, wv);
   tb.init(ldb * 2, b0, bmax, wv);
-  gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(A + a0 * lda), tb, reinterpret_cast<const char*>(B + b0 * ldb),
-                (int)(K / BK), lds);
+  return gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(A + a0 * lda), tb,
+                       reinterpret_cast<const char*>(B + b0 * ldb), (int)(K / BK), lds, tail);
 }
 
 // acc += A[a0:a0+256, k0:k0+64 KT] . B[k0:k0+64 KT, c0:c0+256] over KT full stages,
@@ -503,26 +562,6 @@ __device__ __forceinline__ void gemm_nn(f32x16_t (&acc)[4][4], const uint16_t* _
   }
 }
 
-// Waves holding token columns [128 * half, 128 * half + 128) write their fp32 block to
-// LDS as zt[token][vocab] (row kZRow floats).  Caller guarantees wn == half.
-__device__ __forceinline__ void dump_half(const f32x16_t (&acc)[4][4], lds_t* lds) {
-  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
-  const int r = lane & 31, h = lane >> 5;
-  lds_f32* zt = reinterpret_cast<lds_f32*>(lds);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int tl = j * 32 + r;
-        const int vr = wm * 128 + i * 32 + 8 * g + 4 * h;
-        const f32x4_t x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        *reinterpret_cast<__attribute__((address_space(3))) f32x4_t*>(zt + tl * kZRow + vr) = x;
-      }
-}
-
-
 // ------------------------------------------------------------------ head kernel
 
 struct HeadParams {
@@ -554,6 +593,9 @@ struct HeadParams {
   // trows[t] of nt rows; an index outside [0, nt) makes the row's teacher NaN.  null: row t
   const int64_t* trows;
   int64_t nt;
+  // gathered bf16 teacher rows that may lie 4 GiB or more apart: the epilogue reads them
+  // itself instead of loading them into LDS (whose loads take 32-bit offsets)
+  bool tdirect;
   // teacher log-normalisers from the teacher's producer, one per teacher row (kTeacherLse):
   // pass 1 reads no teacher, pass 2 writes partk[N][splits] = sum t (u - z) for KL
   const float* tlse;
@@ -569,10 +611,12 @@ enum { MODE_STATS = 0, MODE_EMIT = 1, MODE_STORE = 2 };
 // values' log-sum-exp partials are formed (STORE)
 enum { kTeacherLse = 1, kStoreLse = 2 };
 
-// Head-kernel LDS beyond the GEMM stages / epilogue dump: per-token running state and
-// per-token constants of the workgroup's 256 tokens (they persist across vocab tiles).
-constexpr int kStateOff = kDumpLds;                   // [256][8] fp32: mz sz mu su A | arate
-constexpr int kConstOff = kStateOff + 256 * 8 * 4;    // [256][8] fp32: lzl lul cp ct cy
+// Head-kernel LDS beyond the GEMM stages: per-token running state and per-token
+// constants of the workgroup's 256 tokens (they persist across vocab tiles).  The state
+// is kept per vocab half (the two waves holding a token each cover 128 of a tile's 256
+// vocab entries) and the halves are merged once, after the last tile.
+constexpr int kStateOff = kGemmLds;                   // [2][256][8] fp32: mz sz mu su A | arate kl
+constexpr int kConstOff = kStateOff + 2 * 256 * 8 * 4;  // [256][8] fp32: lzl lul cp ct cy zy
 constexpr int kLabelOff = kConstOff + 256 * 8 * 4;    // [256] int64 labels
 constexpr int kPrevOff = kLabelOff + 256 * 8;        // [256] int32 W1 rows (ids clamped to [0, V))
 constexpr int kBadOff = kPrevOff + 256 * 4;          // [256] uint8: id outside [0, V)
@@ -581,40 +625,40 @@ constexpr int kTbadOff = kTrowOff + 256 * 4;        // [256] uint8: teacher (STO
 constexpr int kHrowOff = kTbadOff + 256;            // [256] int32 gathered B rows (MODE_STORE)
 constexpr int kHeadLdsBytes = kHrowOff + 256 * 4;
 static_assert(kHeadLdsBytes <= 160 * 1024, "head kernel LDS");
-static_assert(kGemmLds <= kDumpLds, "the dump region covers the GEMM stages");
 
-// Butterfly partner within groups of 8 lanes, by DPP: step 0 swaps lanes 2i <-> 2i+1
-// (quad_perm [1,0,3,2]), step 1 swaps i <-> i^2 inside a quad (quad_perm [2,3,0,1]),
-// step 2 mirrors the 8 lanes (row_half_mirror: i <-> 7-i).  After steps 0 and 1 every
-// lane of a quad holds the same value, so the mirror pairs the two quads exactly as an
-// xor-4 exchange would.
-template <int STEP>
-__device__ __forceinline__ float dpp_partner(float x) {
-  constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : 0x141;
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false));
+// Lanes l and l ^ 32 hold the same token (vocab entries 4 h .. 4 h + 3 of each 8-entry
+// chunk, h = l / 32).  v_permlane32_swap hands every lane both lanes' values in the same
+// order, so a symmetric merge of the two leaves identical bits in both.
+__device__ __forceinline__ void half_pair(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
 }
 
-template <int STEP>
-__device__ __forceinline__ PairState pair_partner(const PairState& a) {
-  return {dpp_partner<STEP>(a.mz), dpp_partner<STEP>(a.sz), dpp_partner<STEP>(a.mu), dpp_partner<STEP>(a.su),
-          dpp_partner<STEP>(a.A)};
+__device__ __forceinline__ float half_sum(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return a + b;
 }
 
-// Combine over the 8 lanes of a row group; pair_merge is symmetric, so all 8 lanes end
-// with identical bits.
-__device__ __forceinline__ PairState pair_reduce8(PairState a) {
-  a = pair_merge(a, pair_partner<0>(a));
-  a = pair_merge(a, pair_partner<1>(a));
-  return pair_merge(a, pair_partner<2>(a));
+__device__ __forceinline__ PairState half_merge(const PairState& s) {
+  PairState a, b;
+  half_pair(s.mz, a.mz, b.mz);
+  half_pair(s.sz, a.sz, b.sz);
+  half_pair(s.mu, a.mu, b.mu);
+  half_pair(s.su, a.su, b.su);
+  half_pair(s.A, a.A, b.A);
+  return pair_merge(a, b);
 }
 
-__device__ __forceinline__ float sum_reduce8(float x) {
-  x += dpp_partner<0>(x);
-  x += dpp_partner<1>(x);
-  return x + dpp_partner<2>(x);
+__device__ __forceinline__ LseState half_merge(const LseState& s) {
+  LseState a, b;
+  half_pair(s.m, a.m, b.m);
+  half_pair(s.s, a.s, b.s);
+  return lse_merge(a, b);
 }
 
-// One distribution's online (max, sum-exp): fold W values, and combine over 8 lanes.
+// One distribution's online (max, sum-exp) over W values.
 template <int W>
 __device__ __forceinline__ void lse_update(LseState& st, const float* z) {
   float b = z[0];
@@ -628,218 +672,457 @@ __device__ __forceinline__ void lse_update(LseState& st, const float* z) {
   st = {m, s};
 }
 
-__device__ __forceinline__ LseState lse_reduce8(LseState a) {
-  a = lse_merge(a, LseState{dpp_partner<0>(a.m), dpp_partner<0>(a.s)});
-  a = lse_merge(a, LseState{dpp_partner<1>(a.m), dpp_partner<1>(a.s)});
-  return lse_merge(a, LseState{dpp_partner<2>(a.m), dpp_partner<2>(a.s)});
+// pair_update<32> / lse_update<32> with f(g) called after each group of 8 exponentials
+// (the same arithmetic in the same order; the group's sums are pinned before the call)
+template <typename F>
+__device__ __forceinline__ void pair_update32(PairState& st, const float* z, const float* u, F&& f) {
+  float bz = z[0], bu = u[0];
+#pragma unroll
+  for (int i = 1; i < 32; ++i) {
+    bz = fmaxf(bz, z[i]);
+    bu = fmaxf(bu, u[i]);
+  }
+  const float mz = fmaxf(st.mz, bz);
+  const float mu = fmaxf(st.mu, bu);
+  const float mzl = mz * kLog2e, mul = mu * kLog2e;
+  float sz = st.sz * fast_exp2((st.mz - mz) * kLog2e);
+  const float cu = fast_exp2((st.mu - mu) * kLog2e);
+  float su = st.su * cu;
+  float A = st.A * cu;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+#pragma unroll
+    for (int i = 8 * g; i < 8 * g + 8; ++i) {
+      sz += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mzl));
+      const float e = fast_exp2(__builtin_fmaf(u[i], kLog2e, -mul));
+      su += e;
+      A = __builtin_fmaf(e, u[i] - z[i], A);
+    }
+    asm volatile("" : "+v"(sz), "+v"(su), "+v"(A));
+    f(g);
+  }
+  st = {mz, sz, mu, su, A};
 }
 
-// Objective epilogue for one 128-token half of the tile, dumped in LDS as
-// zt[token][vocab] (kZRow floats per token).  Wave w owns tokens 32w .. 32w + 31 of the
-// half in four groups of eight; in a group, lane 8r + c takes token 8g + r and the
-// 16-byte chunks c, c + 8, c + 16, c + 24 of its 256 vocab entries, so each global
-// load or store instruction covers eight rows x 128 contiguous bytes.  The eight lanes
-// of a row combine their partial sums with xor shuffles (a symmetric merge, so every
-// lane ends with the same bits) and lane 0 of the row folds the tile into the token's
-// running state in LDS.  Sums over a tile are formed locally first: one running fp32
-// sum over a whole vocab range (up to ~10^5 terms) would lose the many small terms.
-// V % 8 == 0, so each 8-entry chunk is wholly inside or outside the vocabulary.
-// A row of zeros standing in for the dense Markov addend when there is none, so the
-// epilogue's addend loads and adds need no branch (the widest read is 512 bytes).
-// (Not const: in the global address space like the addend, so the loads stay global.)
+template <typename F>
+__device__ __forceinline__ void lse_update32(LseState& st, const float* z, F&& f) {
+  float b = z[0];
+#pragma unroll
+  for (int i = 1; i < 32; ++i) b = fmaxf(b, z[i]);
+  const float m = fmaxf(st.m, b);
+  const float ml = m * kLog2e;
+  float s = st.s * fast_exp2((st.m - m) * kLog2e);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+#pragma unroll
+    for (int i = 8 * g; i < 8 * g + 8; ++i) s += fast_exp2(__builtin_fmaf(z[i], kLog2e, -ml));
+    asm volatile("" : "+v"(s));
+    f(g);
+  }
+  st = {m, s};
+}
+
+// ---- the epilogue's stream
+//
+// The epilogue works on the accumulators where the MFMAs left them: lane 32 h + r of wave
+// (wm, wn) holds, for each 32-token column block j, token 128 wn + 32 j + r at the vocab
+// entries 128 wm + 32 i + 8 g + 4 h + q (i, g, q = 0..3) as acc[i][j][4 g + q].  It runs
+// in four steps; step s takes column block s of both 128-token halves, 64 tokens.  Their
+// Markov and teacher rows (the tile's 256 entries: 512 bytes of bf16 per row) come
+// straight into LDS, into the step's slot: one of the two 64 KB GEMM stage buffers, with
+// the Markov rows at +0 and the teacher rows at +kSlotU.  Step 0 is loaded during the
+// GEMM's last stages (gemm_nt_tiles' tail).  Step s + 1 goes into the other slot while step
+// s is worked, one load after each piece of work: issued at once, a step's loads filled
+// the memory queue of the CU and stalled the wave's issue for about as long as the work.
+// (These rows come from HBM, unlike the GEMM's operands, which mostly hit the L2.)
+//
+// A slot half holds 32 blocks of 1 KB, each written by one 64-lane load: block b holds
+// step tokens 2b and 2b + 1 (step token e is tile token 128 (e / 32) + 32 s + e % 32), and
+// its 16-byte slot 32 pb + (c ^ sw) holds chunk c (entries 8c .. 8c + 7) of token 2b + pb,
+// sw = 2 (b & 7) + pb.  The lane reading chunk c of token 32 wn + r finds its 8 bytes at
+// 16 KB wn + 512 r + 16 (c ^ (r & 15)) + 8 h, so the 16 lanes r = 0..15 (or 16..31) of one
+// read hit 16 distinct 16-byte bank groups.
+//
+// EMIT and STORE write their bf16 outputs over the Markov rows they read (each lane over
+// its own 8 bytes), then read them back as whole 256-byte row pieces (16 lanes per token,
+// the wave's vocab half) and store those as coalesced rows.  Every lane stores (out-of-
+// range lanes into a sink), so the next step's wait can leave exactly these eight stores
+// in flight.
+constexpr int kSlotU = 64 * 512;   // teacher rows after the 64 Markov rows
+
+// A row of zeros standing in for the dense Markov addend when there is none, so every step
+// loads the same number of blocks (1 KB: the widest offset is 496 + 16 bytes).
 __device__ uint4 kZeroRow[64] = {};
 
-template <int MODE, typename TT, int FLAGS, bool FULL>
-__device__ __forceinline__ void epilogue_half(const HeadParams& p, lds_t* lds, int half, int64_t t0, int64_t v0) {
+// Where the epilogue's out-of-range lanes store (their values are never read).
+__device__ u32x4_t kStoreSink[64];
+
+// One 64-lane load into the 1 KB LDS block dst of block b: lane l fetches chunk
+// c = (l % 32) ^ (2 (b & 7) + l / 32), entries 8c .. 8c + 7 of the tile, of the row at byte
+// offset `row` from the uniform tile base (chunks at or past v - v0 re-read chunk 0).
+__device__ __forceinline__ void stream_dma(const char* base, uint32_t row, int64_t vleft, lds_t* dst, int b,
+                                           int lane) {
+  const int c = (lane & 31) ^ (2 * (b & 7) + (lane >> 5));
+  dma16(base, row + (uint32_t)((8 * c < vleft ? c : 0) * 16), dst);
+}
+
+// Uniform operands of the stream loads of one tile, read from the kernel arguments where
+// they are used (see StreamTail::bases).
+struct StreamBases {
+  const char* mbase;   // Markov rows: the tile's first row at column v0 (or the zero row)
+  const char* ubase;   // teacher rows: likewise, or the teacher's row 0 for gathered rows
+  uint32_t mld, uld;   // row pitches in bytes (0 for the zero row)
+  int umode;           // 0: the tile's rows, 1: gathered rows, 2: none (zero row)
+  int rlast;           // the tile's last row below N (rows past it re-read it)
+  int64_t vleft;       // V - v0
+};
+
+template <int MODE, typename TT, int FLAGS>
+struct StreamTail {
   // the teacher is read in pass 2, and in pass 1 unless its log-normaliser is given
-  constexpr bool kReadU = MODE == MODE_EMIT || (MODE == MODE_STATS && !(FLAGS & kTeacherLse));
-  const lds_f32* zt = reinterpret_cast<const lds_f32*>(lds);
-  lds_f32* state = reinterpret_cast<lds_f32*>(lds + kStateOff);
+  static constexpr bool kReadU = MODE == MODE_EMIT || (MODE == MODE_STATS && !(FLAGS & kTeacherLse));
+  // bf16 teacher rows come through LDS; fp32 rows are read by the epilogue itself
+  static constexpr bool kDmaU = kReadU && sizeof(TT) == 2;
+  static constexpr int kLoads = kDmaU ? 16 : 8;   // loads per wave per step
+  const lds_t* lds;
+  int64_t t0, v0;
+  bool on;
+  // the thread index, opaque to the compiler: address arithmetic derived from it stays in
+  // the vocab-tile loop instead of being hoisted out and kept live across the K loop
+  int tid;
+
+  // The bases, from the kernel arguments (scalar loads) and opaque copies of t0 and v0, so
+  // that nothing of them is computed ahead and held across the K loop.  Offsets are 32-bit
+  // from a uniform base: the tile's first row (rows within 256 of it), or the teacher's row
+  // 0 for gathered rows (all within 4 GiB unless tdirect, where the epilogue reads them).
+  __device__ __forceinline__ StreamBases bases() const {
+    const __attribute__((address_space(4))) HeadParams* kp =
+        (const __attribute__((address_space(4))) HeadParams*)__builtin_amdgcn_kernarg_segment_ptr();
+    int64_t t0o = t0, v0o = v0;
+    asm volatile("" : "+s"(kp), "+s"(t0o), "+s"(v0o));
+    StreamBases sb;
+    const uint16_t* m = kp->markov;
+    sb.mbase = m ? reinterpret_cast<const char*>(m + t0o * kp->ldm + v0o) : reinterpret_cast<const char*>(kZeroRow);
+    sb.mld = m ? (uint32_t)(kp->ldm * 2) : 0u;
+    sb.rlast = (int)(kp->n - 1 - t0o);
+    sb.vleft = kp->v - v0o;
+    sb.umode = 2;
+    sb.ubase = reinterpret_cast<const char*>(kZeroRow);
+    sb.uld = 0;
+    if (kDmaU && !kp->tdirect) {
+      const uint16_t* u = static_cast<const uint16_t*>(kp->teacher);
+      sb.umode = kp->trows ? 1 : 0;
+      sb.ubase = reinterpret_cast<const char*>(kp->trows ? u + v0o : u + t0o * kp->ldt + v0o);
+      sb.uld = (uint32_t)(kp->ldt * 2);
+    }
+    return sb;
+  }
+
+  // load i (0..7) of this wave's Markov (region 0) or teacher (region 1) rows of step s
+  __device__ __forceinline__ void load(const StreamBases& sb, int s, int region, int i, lds_t* slot) const {
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int b = 8 * wv + i;
+    const int tk = (b >> 4) * 128 + 32 * s + 2 * (b & 15) + (lane >> 5);   // this lane's token
+    const int rl = tk < sb.rlast ? tk : sb.rlast;
+    lds_t* dst = slot + (region ? kSlotU : 0) + b * 1024;
+    if (region == 0) {
+      stream_dma(sb.mbase, (uint32_t)rl * sb.mld, sb.vleft, dst, b, lane);
+    } else if (kDmaU) {
+      uint32_t row = (uint32_t)rl * sb.uld;
+      if (sb.umode == 1)   // gathered teacher rows (checked and clamped at kernel start)
+        row = (uint32_t)reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk] * sb.uld;
+      stream_dma(sb.ubase, row, sb.vleft, dst, b, lane);
+    }
+  }
+  __device__ __forceinline__ void load_step(int s, lds_t* slot) const {
+    const StreamBases sb = bases();
+#pragma unroll
+    for (int ci = 0; ci < 16; ++ci) load_part(sb, s, ci, slot);
+  }
+  // gemm_nt_tiles' tail: part 0 = step 0's Markov rows, 1 = step 0's teacher rows
+  __device__ __forceinline__ void issue(const StreamBases& sb, int part, int i, lds_t* slot) const {
+    load(sb, 0, part, i, slot);
+  }
+  // load ci (0..15) of step s, the loads of a step spread over the previous step's work:
+  // Markov load ci / 2 for even ci, teacher load ci / 2 for odd ci (none without them)
+  __device__ __forceinline__ void load_part(const StreamBases& sb, int s, int ci, lds_t* slot) const {
+    if ((ci & 1) == 0 || kDmaU) load(sb, s, ci & 1, ci >> 1, slot);
+  }
+};
+
+typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
+
+// Objective epilogue of one 256 x 256 tile (layout above).  Each lane folds its token's
+// 64 entries per step locally, the two lanes of a token combine (half_merge / half_sum),
+// and the lane of the lower half folds the result into the token's running state for
+// this wave's vocab half.  Sums over a tile are formed locally first: one running fp32
+// sum over a whole vocab range (up to ~10^5 terms) would lose the many small terms.
+// V % 8 == 0, so each 8-entry chunk is wholly inside or outside the vocabulary.
+// `pre`: step 0 was loaded by the GEMM's tail (otherwise the K loop ended with a full
+// barrier and it is loaded here).  Ends with every wave's LDS reads done.
+template <int MODE, typename TT, int FLAGS, bool FULL>
+__device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, const f32x16_t (&acc)[4][4],
+                                              const StreamTail<MODE, TT, FLAGS>& st, int KT, bool pre) {
+  using ST = StreamTail<MODE, TT, FLAGS>;
+  constexpr bool kReadU = ST::kReadU, kDmaU = ST::kDmaU;
+  constexpr bool kOut = MODE == MODE_EMIT || MODE == MODE_STORE;
+  const int64_t t0 = st.t0, v0 = st.v0;
+  const int wv = __builtin_amdgcn_readfirstlane(st.tid >> 6);
+  const int lane = st.tid & 63;
+  const int wm = wv >> 1, wn = wv & 1;
+  lds_f32* state = reinterpret_cast<lds_f32*>(lds + kStateOff) + wm * 256 * 8;
   const lds_f32* cst = reinterpret_cast<const lds_f32*>(lds + kConstOff);
   const __attribute__((address_space(3))) int64_t* lab =
       reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(lds + kLabelOff);
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r8 = lane >> 3, c8 = lane & 7;
-  const bool has_m = p.markov != nullptr;   // kernel argument: uniform
-  // FULL: the tile holds no entry past the vocabulary, so nothing is masked
-  // this lane's chunks (the same in every group): loads are unconditional (chunks past V
-  // re-read the row's first chunk) and the values are masked afterwards
-  bool ok[4];
-  int vc[4];
+  const __attribute__((address_space(3))) uint8_t* badf =
+      reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kBadOff);
+  const __attribute__((address_space(3))) uint8_t* tbadf =
+      reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kTbadOff);
+  auto slot = [&](int s) -> lds_t* { return lds + ((KT + s) & 1) * 2 * kStageBytes; };
+  if (!pre) st.load_step(0, slot(0));
+  // outputs go through LDS and out as rows (EMIT without dl writes nothing)
+  const bool write = MODE == MODE_STORE || (MODE == MODE_EMIT && p.dl != nullptr);
+  uint16_t* const out = MODE == MODE_STORE ? p.out : p.dl;
+  const int64_t ldo = MODE == MODE_STORE ? p.ldo : p.ldd;
+  const float nan = __builtin_nanf("");
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int vl = 8 * c8 + 64 * k;
-    ok[k] = v0 + vl < p.v;
-    vc[k] = ok[k] ? vl : 0;
-  }
-  // the Markov and teacher rows of group g's token: issued one group ahead, so two
-  // groups' loads are in flight while a group is processed
-  auto mrow_of = [&](int g) -> const uint16_t* {
-    const int64_t t = t0 + half * 128 + 32 * w + 8 * g + r8;
-    const int64_t trow = t < p.n ? t : p.n - 1;
-    return has_m ? p.markov + trow * p.ldm + v0 : reinterpret_cast<const uint16_t*>(kZeroRow);
-  };
-  auto urow_of = [&](int g) -> const TT* {
-    const int tk = half * 128 + 32 * w + 8 * g + r8;
-    const int trw = reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk];
-    return kReadU ? static_cast<const TT*>(p.teacher) + (int64_t)trw * p.ldt + v0 : nullptr;
-  };
-  // two statically indexed buffers (the group loop is unrolled), so no copy of a
-  // loaded register forces its wait early
-  Raw8<uint16_t> mbuf[2][4];
-  Raw8<TT> ubuf[2][4];
-  auto issue = [&](int g, int b) {
-    const uint16_t* mr = mrow_of(g);
-    const TT* ur = urow_of(g);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (kReadU) ubuf[b][k].load(ur + vc[k]);
-      mbuf[b][k].load(mr + vc[k]);
+  for (int s = 0; s < 4; ++s) {
+    // this step's loads landed in every wave (after step 0, the previous step's eight row
+    // stores may still fly), and every wave is done with the previous step's slot, which
+    // the next step's loads go to while this step works
+    if (s == 0) {
+      vm_barrier<0>();
+      // the K loop's last MFMAs may still be writing accumulators that the volatile reads
+      // below take without the compiler's hazard wait states: 24 wait states cover the
+      // 16-pass 32x32 MFMA's 18
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    } else if (kOut && write) {
+      vm_barrier<8>();
+    } else {
+      vm_barrier<0>();
     }
-  };
-  // prefetch where the registers allow it (bf16 teacher; not the teacher-once pass 2,
-  // which also carries the KL sum): otherwise each group issues its own loads first
-  constexpr bool kPrefetch = sizeof(TT) == 2 && !(MODE == MODE_EMIT && (FLAGS & kTeacherLse));
-  if (kPrefetch) issue(0, 0);
-  // pairs of groups in a rolled loop: buffer 0 always holds the even group and buffer 1
-  // the odd one, so the loop carries the prefetch in the same registers
-#pragma unroll 1
-  for (int g2 = 0; g2 < 4; g2 += 2)
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int g = g2 + j;                    // group; its buffer is j (g2 is even)
-    const int tl = 32 * w + 8 * g + r8;      // token within the half
-    const int tk = half * 128 + tl;          // token within the workgroup tile
+    // per-step copy of the lane index, opaque: the step's address arithmetic stays after
+    // its barrier instead of being computed early and held in registers
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r = ln & 31, h = ln >> 5;
+    // this lane's 8 bytes of chunk k (= 4 i + g) of its vocab half sit at lb + 16 (k ^ (r & 15))
+    const int lb = wn * 16384 + r * 512 + wm * 256 + 8 * h;
+    lds_t* sl = slot(s);
+    // load ci of the next step, issued between this step's chunks so that the wave never
+    // waits on a full memory queue with work left (a step's loads at once stalled issue)
+    StreamBases sbn{};
+    if (s < 3) sbn = st.bases();
+    auto next = [&](int ci) {
+      if (s < 3) {
+        __builtin_amdgcn_sched_barrier(0);
+        st.load_part(sbn, s + 1, ci, slot(s + 1));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    const int tk = wn * 128 + 32 * s + r;   // this lane's token
     const int64_t t = t0 + tk;
     const bool tok_ok = t < p.n;
-    const lds_f32* zr = zt + tl * kZRow;
-    const uint16_t* mrow = mrow_of(g);
-    const bool ubad = reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kTbadOff)[tk];
-    const TT* urow = urow_of(g);
-    float z[32], u[32];
-    if (!kPrefetch) issue(g, j);
-    else if (g < 3) issue(g + 1, j ^ 1);
-    const Raw8<uint16_t>(&mraw)[4] = mbuf[j];
-    const Raw8<TT>(&uraw)[4] = ubuf[j];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int vl = 8 * c8 + 64 * k;
-      const f32x4_t x0 = *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(zr + vl);
-      const f32x4_t x1 = *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(zr + vl + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { z[8 * k + e] = x0[e]; z[8 * k + 4 + e] = x1[e]; }
-    }
-    // A previous-token id outside [0, V) has no Markov row and a teacher row outside the
-    // teacher tensor has no logits: the row's pass-1 state is made NaN (below), so its
-    // log-normaliser, loss terms and pass-2 dl and accept rate are NaN and the loss reports
-    // the bad input (the reference's embedding lookup and gather raise).
-    const bool bad = reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(lds + kBadOff)[tk] != 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float mk[8];
-      mraw[k].unpack(mk);
-      if (kReadU) uraw[k].unpack(u + 8 * k);
-      if (MODE == MODE_STORE) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // a gathered B row outside its matrix: the output row is NaN
-          const float zk = ubad ? __builtin_nanf("") : z[8 * k + e] + mk[e];
-          z[8 * k + e] = ok[k] ? zk : kNegBig;
-        }
-      } else if (FULL) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) z[8 * k + e] += mk[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          z[8 * k + e] = ok[k] ? z[8 * k + e] + mk[e] : kNegBig;
-          if (kReadU) u[8 * k + e] = ok[k] ? u[8 * k + e] : kNegBig;
-        }
-      }
-    }
-    if (MODE == MODE_STORE) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (ok[k] && tok_ok) store8(p.out + t * p.ldo + v0 + 8 * c8 + 64 * k, z + 8 * k);
-      if (FLAGS & kStoreLse) {
-        // log-sum-exp of the values as stored (bf16), which is what a consumer reads
-#pragma unroll
-        for (int i = 0; i < 32; ++i) z[i] = bf16_to_f32(f32_to_bf16(z[i]));
-        LseState loc = {kNegBig, 0.f};
-        if (ok[0]) lse_update<32>(loc, z);
-        loc = lse_reduce8(loc);
-        if (c8 == 0) {
-          lds_f32* sr = state + tk * 8;
-          const LseState r = lse_merge(LseState{sr[0], sr[1]}, loc);
-          sr[0] = r.m; sr[1] = r.s;
-        }
-      }
-      continue;
-    }
-    const int64_t y = lab[tk];
+    const bool bad = badf[tk] != 0;
+    const bool ubad = tbadf[tk] != 0;
+    const int64_t y = MODE == MODE_STORE ? -1 : lab[tk];
     const int64_t yr = y - v0;
-    // this lane holds z_y (labels outside [0, V) match nothing; the merge flags them)
-    const bool mine = yr >= 0 && yr < BM && y < p.v && ((yr >> 3) & 7) == c8 && tok_ok;
-    const float nan = __builtin_nanf("");
-    if (MODE == MODE_STATS && (FLAGS & kTeacherLse)) {
-      LseState loc = {kNegBig, 0.f};
-      if (FULL || ok[0]) lse_update<32>(loc, z);
-      loc = lse_reduce8(loc);
-      if (bad) loc = {nan, nan};
-      if (c8 == 0) {
-        lds_f32* sr = state + tk * 8;
-        const LseState r = lse_merge(LseState{sr[0], sr[1]}, loc);
-        sr[0] = r.m; sr[1] = r.s;
+    // this lane holds entry y (labels outside [0, V) match nothing; the merge flags them)
+    const bool mine = MODE != MODE_STORE && tok_ok && yr >= 0 && yr < BM && y < p.v && (int)(yr >> 7) == wm &&
+                      (int)((yr >> 2) & 1) == h;
+    const lds_f32* cr = cst + tk * 8;
+    float lzl = 0.f, lul = 0.f, cp = 0.f, ct = 0.f;
+    if (MODE == MODE_EMIT) {
+      lzl = cr[0]; lul = cr[1]; cp = cr[2]; ct = cr[3];
+    }
+    const TT* urow = nullptr;
+    if (kReadU && (!kDmaU || p.tdirect)) {
+      const int trw = reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk];
+      urow = static_cast<const TT*>(p.teacher) + (int64_t)trw * p.ldt + v0;
+    }
+    PairState ploc = pair_init();
+    LseState lloc = {kNegBig, 0.f};
+    float aloc = 0.f, kloc = 0.f;
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs) {
+      __builtin_amdgcn_sched_barrier(0);   // one half-step's values live at a time
+      // the accumulators are read where they are used (volatile: not hoisted above the
+      // step's barrier, which would hold all 256 in VGPRs at once)
+      float z[32], u[32];
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(z[16 * ii + e]) : "a"(acc[2 * hs + ii][s][e]));
+      u32x2v_t mraw[8], uraw[8];
+      int off[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int k = 8 * hs + c;   // chunk 4 i + g of the wave's vocab half
+        off[c] = lb + ((k ^ (r & 15)) << 4);
+        mraw[c] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2v_t*>(sl + off[c]);
       }
-      if (mine) p.zy[t] = bad ? nan : zr[yr] + bf16_to_f32(mrow[yr]);   // rare: the label is in this tile
-    } else if (MODE == MODE_STATS) {
-      PairState loc = pair_init();
-      // ok[] falls with k: a lane with no valid chunk keeps the empty state (an update
-      // with every entry at the sentinel would form inf - inf)
-      if (FULL || ok[0]) pair_update<32>(loc, z, u);
-      loc = pair_reduce8(loc);
+      if (kDmaU) {
+        if (p.tdirect) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const int vl = wm * 128 + 8 * (8 * hs + c) + 4 * h;
+            const bool in = FULL || v0 + wm * 128 + 8 * (8 * hs + c) < p.v;
+            uraw[c] = *reinterpret_cast<const u32x2v_t*>(urow + (in ? vl : 0));
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+            uraw[c] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2v_t*>(sl + kSlotU + off[c]);
+        }
+      }
+      // chunk c is inside the vocabulary; the first one of the half-step decides whether
+      // the lane has any entry (a fold over sentinels only would form inf - inf)
+      bool okc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) okc[c] = FULL || v0 + wm * 128 + 8 * (8 * hs + c) < p.v;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float mk[4];
+        mk[0] = bf16_lo(mraw[c][0]); mk[1] = bf16_hi(mraw[c][0]);
+        mk[2] = bf16_lo(mraw[c][1]); mk[3] = bf16_hi(mraw[c][1]);
+        if (kDmaU) {
+          u[4 * c + 0] = bf16_lo(uraw[c][0]); u[4 * c + 1] = bf16_hi(uraw[c][0]);
+          u[4 * c + 2] = bf16_lo(uraw[c][1]); u[4 * c + 3] = bf16_hi(uraw[c][1]);
+        } else if (kReadU) {
+          const int vl = wm * 128 + 8 * (8 * hs + c) + 4 * h;
+          const float4 x = *reinterpret_cast<const float4*>(urow + (okc[c] ? vl : 0));
+          u[4 * c + 0] = x.x; u[4 * c + 1] = x.y; u[4 * c + 2] = x.z; u[4 * c + 3] = x.w;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float& zq = z[4 * c + q];
+          if (MODE == MODE_STORE) {
+            // a gathered B row outside its matrix: the output row is NaN
+            zq = okc[c] ? (ubad ? nan : zq + mk[q]) : kNegBig;
+          } else {
+            zq = okc[c] ? zq + mk[q] : kNegBig;
+            if (kReadU && !FULL) u[4 * c + q] = okc[c] ? u[4 * c + q] : kNegBig;
+          }
+        }
+      }
+      const bool any = FULL || okc[0];
+      if (MODE == MODE_STATS) {
+        auto next2 = [&](int g) {
+          next(2 * (4 * hs + g));
+          next(2 * (4 * hs + g) + 1);
+        };
+        if (FLAGS & kTeacherLse) {
+          if (any) lse_update32(lloc, z, next2);
+          else for (int g = 0; g < 4; ++g) next2(g);
+        } else {
+          if (any) pair_update32(ploc, z, u, next2);
+          else for (int g = 0; g < 4; ++g) next2(g);
+        }
+        // the label entry, when this half-step holds it (rare: the label is in this tile)
+        const bool here = mine && (int)((yr >> 6) & 1) == hs;
+        if (__any(here)) {
+          const int idx = (int)((((yr >> 5) & 1) << 4) | (((yr >> 3) & 3) << 2) | (yr & 3));
+          float zv = 0.f;
+#pragma unroll
+          for (int k2 = 0; k2 < 32; ++k2) zv = k2 == idx ? z[k2] : zv;
+          if (here) p.zy[t] = bad ? nan : zv;
+        }
+      } else if (MODE == MODE_EMIT) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          float d[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float zq = z[4 * c + q], uq = u[4 * c + q];
+            const float pp = fast_exp2(__builtin_fmaf(zq, kLog2e, -lzl));
+            const float tt = fast_exp2(__builtin_fmaf(uq, kLog2e, -lul));
+            aloc += min_nonneg(pp, tt);
+            // KL's sum t (u - z) (entries past V: t = 0 and u = z)
+            if (FLAGS & kTeacherLse) kloc = __builtin_fmaf(tt, uq - zq, kloc);
+            d[q] = __builtin_fmaf(cp, pp, -ct * tt);
+          }
+          // written even without dl (never read back then): no branch in the loop
+          const u32x2v_t o = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3])};
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2v_t*>(sl + off[c]) = o;
+          // the chunk's sums are formed here, not deferred with every chunk's values live
+          asm volatile("" : "+v"(aloc), "+v"(kloc));
+          next(8 * hs + c);
+        }
+      } else {   // MODE_STORE
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const u32x2v_t o = {pack_bf16x2(z[4 * c], z[4 * c + 1]), pack_bf16x2(z[4 * c + 2], z[4 * c + 3])};
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2v_t*>(sl + off[c]) = o;
+          next(8 * hs + c);
+        }
+        if (FLAGS & kStoreLse) {
+          // log-sum-exp of the values as stored (bf16), which is what a consumer reads
+#pragma unroll
+          for (int i = 0; i < 32; ++i) z[i] = bf16_to_f32(f32_to_bf16(z[i]));
+          if (any) lse_update<32>(lloc, z);
+        }
+      }
+    }
+    // fold the step into the token's state (lanes of the lower half write)
+    if (MODE == MODE_STATS && !(FLAGS & kTeacherLse)) {
+      PairState loc = half_merge(ploc);
       if (bad) { loc.mz = nan; loc.sz = nan; }
       if (ubad) { loc.mu = nan; loc.su = nan; loc.A = nan; }
-      if (c8 == 0) {
+      if (h == 0) {
         lds_f32* sr = state + tk * 8;
-        const PairState r = pair_merge(PairState{sr[0], sr[1], sr[2], sr[3], sr[4]}, loc);
-        sr[0] = r.mz; sr[1] = r.sz; sr[2] = r.mu; sr[3] = r.su; sr[4] = r.A;
+        const PairState m2 = pair_merge(PairState{sr[0], sr[1], sr[2], sr[3], sr[4]}, loc);
+        sr[0] = m2.mz; sr[1] = m2.sz; sr[2] = m2.mu; sr[3] = m2.su; sr[4] = m2.A;
       }
-      if (mine) p.zy[t] = bad ? nan : zr[yr] + bf16_to_f32(mrow[yr]);   // rare: the label is in this tile
-    } else {
-      const lds_f32* cr = cst + tk * 8;
-      const float lzl = cr[0], lul = cr[1], cp = cr[2], ct = cr[3], cy = cr[4];
-      float aloc = 0.f, kloc = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float d[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pp = fast_exp2(__builtin_fmaf(z[8 * k + e], kLog2e, -lzl));
-          const float tt = fast_exp2(__builtin_fmaf(u[8 * k + e], kLog2e, -lul));
-          aloc += min_nonneg(pp, tt);
-          // KL's sum t (u - z) (entries past V: t = 0 and u = z)
-          if (FLAGS & kTeacherLse) kloc = __builtin_fmaf(tt, u[8 * k + e] - z[8 * k + e], kloc);
-          d[e] = __builtin_fmaf(cp, pp, -ct * tt);
-        }
-        if (p.dl && ok[k] && tok_ok) store8(p.dl + t * p.ldd + v0 + 8 * c8 + 64 * k, d);
+    } else if (MODE == MODE_STATS || (MODE == MODE_STORE && (FLAGS & kStoreLse))) {
+      LseState loc = half_merge(lloc);
+      if (MODE == MODE_STATS && bad) loc = {nan, nan};
+      if (h == 0) {
+        lds_f32* sr = state + tk * 8;
+        const LseState m2 = lse_merge(LseState{sr[0], sr[1]}, loc);
+        sr[0] = m2.m; sr[1] = m2.s;
       }
-      aloc = sum_reduce8(aloc);
-      if (c8 == 0) state[tk * 8] += aloc;
+    } else if (MODE == MODE_EMIT) {
+      aloc = half_sum(aloc);
+      if (h == 0) state[tk * 8] += aloc;
       if (FLAGS & kTeacherLse) {
-        kloc = sum_reduce8(kloc);
-        if (c8 == 0) state[tk * 8 + 1] += kloc;
+        kloc = half_sum(kloc);
+        if (h == 0) state[tk * 8 + 1] += kloc;
       }
-      // the label entry: rewrite dl[y] with the -c_ce term (same lane, after its store)
-      if (mine && p.dl) {   // rare: the label is in this tile (a bad row's NaN comes through its lse)
-        const float zy = zr[yr] + bf16_to_f32(mrow[yr]);
-        const float uy = load1(urow + yr);
-        const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
-        const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
-        store1(p.dl + t * p.ldd + y, __builtin_fmaf(cp, pp, -ct * tt) - cy);
+    }
+    if (kOut && write) {
+      if (MODE == MODE_EMIT && __any(mine)) {
+        // the label entry: rewrite dl[y] with the -c_ce term over this lane's own store
+        // (a bad row's NaN comes through its log-normaliser); z_y is pass 1's value
+        if (mine) {
+          const int k = (int)((yr >> 3) & 15);
+          const int a = lb - 8 * h + ((k ^ (r & 15)) << 4) + 2 * (int)(yr & 7);
+          const float uy = kDmaU && !p.tdirect
+                               ? bf16_to_f32(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+                                     sl + kSlotU + a))
+                               : load1(urow + yr);
+          const float pp = fast_exp2(__builtin_fmaf(cr[5], kLog2e, -lzl));
+          const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
+          *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(sl + a) =
+              f32_to_bf16(__builtin_fmaf(cp, pp, -ct * tt) - cr[4]);
+        }
+      }
+      // read back this wave's rows, 16 lanes per token and 4 tokens per read, and store
+      // them; every lane stores (rows past N and chunks past V into a sink), so a step
+      // always issues exactly eight stores, which the next step's wait counts on
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int r2 = 4 * k + (ln >> 4), cl = ln & 15;
+        const u32x4_t x = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+            sl + (lb - r * 512 - 8 * h) + r2 * 512 + ((cl ^ (r2 & 15)) << 4));
+        const int64_t t2 = t0 + wn * 128 + 32 * s + r2;
+        const int64_t col = v0 + 8 * (wm * 16 + cl);
+        const bool in = t2 < p.n && (FULL || col < p.v);
+        *(in ? reinterpret_cast<u32x4_t*>(out + t2 * ldo + col) : &kStoreSink[ln]) = x;
       }
     }
   }
+  lds_barrier();
 }
 
 template <int MODE, typename TT, int FLAGS>
@@ -852,7 +1135,6 @@ void head_kernel(HeadParams p) {
   const int vt_begin = (int)((int64_t)split * p.vt / p.splits);
   const int vt_end = (int)((int64_t)(split + 1) * p.vt / p.splits);
   const int tid = threadIdx.x;
-  const int wn = (tid >> 6) & 1;
   const int64_t t0 = (int64_t)tile_t * BN;
 
   // per-token state and constants of this workgroup's 256 tokens (thread tid: token tid);
@@ -880,19 +1162,25 @@ void head_kernel(HeadParams p) {
       reinterpret_cast<__attribute__((address_space(3))) int*>(lds + kHrowOff)[tid] = ok ? (int)rr : 0;
   }
   if (MODE == MODE_STORE && (FLAGS & kStoreLse)) {
-    lds_f32* sr = reinterpret_cast<lds_f32*>(lds + kStateOff) + tid * 8;
-    sr[0] = kNegBig;
-    sr[1] = 0.f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      lds_f32* sr = reinterpret_cast<lds_f32*>(lds + kStateOff) + (half * 256 + tid) * 8;
+      sr[0] = kNegBig;
+      sr[1] = 0.f;
+    }
   }
   // gathered B rows are read from LDS by every wave's fill offsets before the first barrier
   if (MODE == MODE_STORE && p.hrows) __syncthreads();
   if (MODE != MODE_STORE) {
     const int64_t t = t0 + tid;
     const int64_t trow = t < p.n ? t : p.n - 1;
-    lds_f32* sr = reinterpret_cast<lds_f32*>(lds + kStateOff) + tid * 8;
     const PairState z0 = pair_init();
-    sr[0] = MODE == MODE_STATS ? z0.mz : 0.f;
-    sr[1] = z0.sz; sr[2] = z0.mu; sr[3] = z0.su; sr[4] = z0.A;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      lds_f32* sr = reinterpret_cast<lds_f32*>(lds + kStateOff) + (half * 256 + tid) * 8;
+      sr[0] = MODE == MODE_STATS ? z0.mz : 0.f;
+      sr[1] = z0.sz; sr[2] = z0.mu; sr[3] = z0.su; sr[4] = z0.A;
+    }
     reinterpret_cast<__attribute__((address_space(3))) int64_t*>(lds + kLabelOff)[tid] = p.labels[trow];
     if (MODE == MODE_EMIT) {
       lds_f32* cr = reinterpret_cast<lds_f32*>(lds + kConstOff) + tid * 8;
@@ -903,6 +1191,7 @@ void head_kernel(HeadParams p) {
       cr[2] = p.labels[trow] == kIgnoreIndex ? w * p.c_kl : w * (p.c_ce + p.c_kl);
       cr[3] = w * p.c_kl;
       cr[4] = w * p.c_ce;
+      cr[5] = p.row_stats[trow * kRowStatWidth + kZy];   // pass 1's z + Markov at the label
     }
   }
 
@@ -910,54 +1199,64 @@ void head_kernel(HeadParams p) {
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int64_t v0 = (int64_t)vt * BM;
     zero_acc(acc);
+    // the epilogue's first two stream steps load during the last K segment's final stages
+    int tid_o = tid;
+    asm volatile("" : "+v"(tid_o));
+    StreamTail<MODE, TT, FLAGS> tail{lds, t0, v0, p.r == 0, tid_o};
+    int KT = (int)(p.d / BK);
+    bool pre;
     if (MODE == MODE_STORE && p.hrows) {   // B = hidden[hrows[t-tile]]
       const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
       DmaTile<256> ta, tb;
       ta.init(p.ldw * 2, v0, p.v, wv);
       tb.init_gather(p.ldh * 2, reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kHrowOff), wv);
-      gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.weight + v0 * p.ldw), tb,
-                    reinterpret_cast<const char*>(p.hidden), (int)(p.d / BK), lds);
+      pre = gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.weight + v0 * p.ldw), tb,
+                          reinterpret_cast<const char*>(p.hidden), KT, lds, tail);
     } else {
-      gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds);
+      pre = gemm_nt(acc, p.weight, p.ldw, v0, p.v, p.hidden, p.ldh, t0, p.n, p.d, lds, tail);
     }
     if (p.r > 0) {   // Markov K segment: W2[v-tile] . W1[prev[t-tile]]^T
       const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
       DmaTile<256> ta, tb;
       ta.init(p.ldw2 * 2, v0, p.v, wv);
       tb.init_gather(p.ldw1 * 2, reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kPrevOff), wv);
-      gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.w2 + v0 * p.ldw2), tb,
-                    reinterpret_cast<const char*>(p.w1), (int)(p.r / BK), lds);
+      tail.on = true;
+      KT = (int)(p.r / BK);
+      pre = gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.w2 + v0 * p.ldw2), tb,
+                          reinterpret_cast<const char*>(p.w1), KT, lds, tail);
     }
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      if (wn == jj) dump_half(acc, lds);
-      __syncthreads();
-      if (v0 + BM <= p.v)
-        epilogue_half<MODE, TT, FLAGS, true>(p, lds, jj, t0, v0);
-      else
-        epilogue_half<MODE, TT, FLAGS, false>(p, lds, jj, t0, v0);
-      __syncthreads();
-    }
+    if (v0 + BM <= p.v)
+      epilogue_tile<MODE, TT, FLAGS, true>(p, lds, acc, tail, KT, pre);
+    else
+      epilogue_tile<MODE, TT, FLAGS, false>(p, lds, acc, tail, KT, pre);
   }
 
   if (MODE == MODE_STORE && !(FLAGS & kStoreLse)) return;
-  // this split's partial of every token (state complete: the last epilogue ended with a barrier)
+  // this split's partial of every token: the two vocab halves' states merged (complete:
+  // the last epilogue ended with a barrier)
   const int64_t t = t0 + tid;
   if (t < p.n) {
-    const lds_f32* sr = reinterpret_cast<const lds_f32*>(lds + kStateOff) + tid * 8;
-    if (MODE == MODE_STATS || MODE == MODE_STORE) {
-      // teacher-free pass 1 and the stored values' partials carry (mz, sz) only
-      const bool pair = MODE == MODE_STATS && !(FLAGS & kTeacherLse);
+    const lds_f32* s0 = reinterpret_cast<const lds_f32*>(lds + kStateOff) + tid * 8;
+    const lds_f32* s1 = s0 + 256 * 8;
+    if (MODE == MODE_STATS && !(FLAGS & kTeacherLse)) {
+      const PairState m2 = pair_merge(PairState{s0[0], s0[1], s0[2], s0[3], s0[4]},
+                                      PairState{s1[0], s1[1], s1[2], s1[3], s1[4]});
       RowPart rp;
-      rp.mz = sr[0]; rp.sz = sr[1];
-      rp.mu = pair ? sr[2] : kNegBig;
-      rp.su = pair ? sr[3] : 0.f;
-      rp.A = pair ? sr[4] : 0.f;
+      rp.mz = m2.mz; rp.sz = m2.sz; rp.mu = m2.mu; rp.su = m2.su; rp.A = m2.A;
+      rp.pad0 = rp.pad1 = rp.pad2 = 0.f;
+      p.part1[t * p.splits + split] = rp;
+    } else if (MODE == MODE_STATS || MODE == MODE_STORE) {
+      // pass 1 with the teacher's log-normaliser given and the stored values' partials
+      // carry (mz, sz) only
+      const LseState m2 = lse_merge(LseState{s0[0], s0[1]}, LseState{s1[0], s1[1]});
+      RowPart rp;
+      rp.mz = m2.m; rp.sz = m2.s;
+      rp.mu = kNegBig; rp.su = 0.f; rp.A = 0.f;
       rp.pad0 = rp.pad1 = rp.pad2 = 0.f;
       p.part1[t * p.splits + split] = rp;
     } else {
-      p.parta[t * p.splits + split] = sr[0];
-      if (FLAGS & kTeacherLse) p.partk[t * p.splits + split] = sr[1];
+      p.parta[t * p.splits + split] = s0[0] + s1[0];
+      if (FLAGS & kTeacherLse) p.partk[t * p.splits + split] = s0[1] + s1[1];
     }
   }
 }
@@ -1190,6 +1489,10 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
 
 template <int MODE, typename TT, int FLAGS = 0>
 hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char* name) {
+  // the epilogue's Markov and teacher loads take 32-bit offsets across a 256-row tile
+  constexpr int64_t kMaxLd = (int64_t)(0xffffffffLL - 1024) / 512;
+  if (p.markov && p.ldm > kMaxLd) return hipErrorInvalidValue;
+  if (StreamTail<MODE, TT, FLAGS>::kDmaU && !p.trows && p.ldt > kMaxLd) return hipErrorInvalidValue;
   static std::atomic<uint64_t> attr_done{0};
   if (const hipError_t e =
           ensure_dynamic_lds(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>), kHeadLdsBytes, attr_done))
@@ -1240,6 +1543,8 @@ HeadParams head_params(const void* hidden, int64_t ldh, const void* weight, int6
   p.dl = static_cast<uint16_t*>(dl); p.ldd = ldd;
   if (ts) {
     p.trows = ts->rows; p.nt = ts->nt; p.tlse = ts->lse;
+    // any two gathered rows within 4 GiB of each other (bf16 rows through LDS)
+    p.tdirect = ts->rows && ts->nt > 1 && (ts->nt - 1) * ldt * 2 + 512 > (int64_t)0xffffffffLL;
   }
   if (factors) {
     p.prev = factors->prev;
@@ -1319,11 +1624,11 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
   p.part2 = reinterpret_cast<float*>(static_cast<char*>(ws) + b_part);
   void* norm_ws = static_cast<char*>(ws) + b_part + b_part2;
   static std::atomic<uint64_t> attr_done{0};
-  if (const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&dh_kernel), kLdsBytes, attr_done))
+  if (const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&dh_kernel), kGemmLds, attr_done))
     return e;
   {
     NS_TIMED("dh_gemm", st);
-    hipLaunchKernelGGL(dh_kernel, dim3(pl.grid), dim3(kThreads), kLdsBytes, st, p);
+    hipLaunchKernelGGL(dh_kernel, dim3(pl.grid), dim3(kThreads), kGemmLds, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
