@@ -53,6 +53,26 @@ def test_gathered_teacher_rows_equal_a_gathered_copy(gpu_lib, tdtype):
     assert torch.equal(s1.row_stats, s2.row_stats) and torch.equal(s1.dlogits, s2.dlogits)
 
 
+def test_gathered_teacher_rows_more_than_4gib_apart(gpu_lib):
+    # A bf16 teacher of 270,000 x 8192 (4.4 GB): gathered rows near both ends are more than
+    # 4 GiB apart, so the head reads them itself instead of loading them into LDS (whose
+    # loads take 32-bit offsets).  Same bar as above: equal to a gathered copy, bit for bit.
+    n, d, v, rows_total = 256, 128, 8192, 270_000
+    hidden, weight, markov, _, slots = synthetic.head_inputs(n, d, v, 36, DEV)
+    g = torch.Generator(device=DEV).manual_seed(37)
+    rows = torch.randint(0, 64, (n,), generator=g, device=DEV)
+    rows[1::2] += rows_total - 64               # alternate between the first and last rows
+    full = torch.empty((rows_total, v), dtype=torch.bfloat16, device=DEV)
+    full[rows] = (3.0 * torch.randn((n, v), generator=g, device=DEV)).bfloat16()
+    o = Objective(block_size=8)
+    m1, s1 = _run(hidden, weight, head.TeacherLogits(full, rows), slots, o, markov_logits=markov)
+    m2, s2 = _run(hidden, weight, full[rows].contiguous(), slots, o, markov_logits=markov)
+    del full
+    for f in FIELDS:
+        assert torch.equal(getattr(m1, f), getattr(m2, f)), f
+    assert torch.equal(s1.row_stats, s2.row_stats) and torch.equal(s1.dlogits, s2.dlogits)
+
+
 def test_teacher_row_out_of_range_poisons_its_row(gpu_lib):
     n, d, v = 64, 128, 2048
     hidden, weight, markov, teacher, slots = synthetic.head_inputs(n, d, v, 33, DEV)
