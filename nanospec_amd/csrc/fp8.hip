@@ -245,6 +245,10 @@ void fp8_head_kernel(Fp8Params p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
+      for (int e = 0; e < 16; ++e) part[j][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
       for (int kk = 0; kk < 2; ++kk) b[j][kk] = rd32(buf(0) + kAStage, wn * 64 + j * 32 + r, kk * 4 + kh * 2);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) a[kk] = rd32(buf(0), wm * 128 + r, kk * 4 + kh * 2);
@@ -257,8 +261,9 @@ void fp8_head_kernel(Fp8Params p) {
       const bool more = t + 1 < KB, fill2 = t + 2 < KB;
       const int kn = more ? t + 1 : t;
       // 16 MFMA slots s = 4 q + 2 j + kk; the pair (q, j) accumulates over the stage's two
-      // 64-K halves, and each pair is folded into the accumulator with the block scale two
-      // slots after it completes, 8 elements per slot (sched_barrier keeps the order)
+      // 64-K halves into part[j], which is folded into the accumulator with the block
+      // scale in slot (q + 1, j, 0), before the next pair overwrites it (sched_barrier
+      // keeps the order)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
@@ -266,6 +271,15 @@ void fp8_head_kernel(Fp8Params p) {
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk) {
             const int s = 4 * q + 2 * j + kk;
+            // block (q - 1, j) (the previous stage's (3, j) when q = 0) is folded with its
+            // scale just before its partial is overwritten: its last MFMA was issued three
+            // slots ago and has completed, so the fold does not wait on the matrix core
+            if (kk == 0) {
+              if (q > 0)
+                fold8(acc[q - 1][j], part[j], c_cur[j], 0), fold8(acc[q - 1][j], part[j], c_cur[j], 8);
+              else   // at t = 0 part[j] and c_prev[j] are 0, which adds nothing
+                fold8(acc[3][j], part[j], c_prev[j], 0), fold8(acc[3][j], part[j], c_prev[j], 8);
+            }
             part[j] = mfma_f8(a[kk], b[j][kk], kk == 0 ? f32x16_t{} : part[j]);
             asm volatile("" : "+v"(part[j]));   // keep the MFMAs in program order
             __builtin_amdgcn_sched_barrier(0);
@@ -273,13 +287,6 @@ void fp8_head_kernel(Fp8Params p) {
               xn[0] = p.xs[xsoff[0] + kn];
               xn[1] = p.xs[xsoff[1] + kn];
               wnx = wsrow[kn];
-            }
-            if (j == 1) {   // block (q, 0) completed two slots ago
-              fold8(acc[q][0], part[0], c_cur[0], kk * 8);
-            } else if (q > 0) {   // block (q - 1, 1)
-              fold8(acc[q - 1][1], part[1], c_cur[1], kk * 8);
-            } else if (t > 0) {   // the previous stage's block (3, 1)
-              fold8(acc[3][1], part[1], c_prev[1], kk * 8);
             }
             // block row q + 1's A fragment kk, after its last use by block (q, 1)
             if (q < 3 && j == 1) a[kk] = rd32(cb, wm * 128 + (q + 1) * 32 + r, kk * 4 + kh * 2);
@@ -313,9 +320,11 @@ void fp8_head_kernel(Fp8Params p) {
       c_cur[0] = xn[0] * wnx;
       c_cur[1] = xn[1] * wnx;
     }
-    // the last stage's block (3, 1)
+    // the last stage's blocks (3, 0) and (3, 1)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[3][1][e] = __builtin_fmaf(c_prev[1], part[1][e], acc[3][1][e]);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[3][j][e] = __builtin_fmaf(c_prev[j], part[j][e], acc[3][j][e]);
     wait_barrier<kWaitAll>();   // no fill in flight, every wave done with the ring
 
     // bf16 tile transposed through LDS in two passes of 128 tokens, then whole 16-byte
