@@ -793,8 +793,10 @@ struct StreamTail {
 
   // The bases, from the kernel arguments (scalar loads) and opaque copies of t0 and v0, so
   // that nothing of them is computed ahead and held across the K loop.  Offsets are 32-bit
-  // from a uniform base: the tile's first row (rows within 256 of it), or the teacher's row
-  // 0 for gathered rows (all within 4 GiB unless tdirect, where the epilogue reads them).
+  // from a uniform base: the tile's first row (rows within 256 of it; the C ABI caps leading
+  // dimensions at 2^23 elements, so 255 rows and a row's 512 bytes stay below 4 GiB), or the
+  // teacher's row 0 for gathered rows (all within 4 GiB unless tdirect, where the epilogue
+  // reads them).
   __device__ __forceinline__ StreamBases bases() const {
     const __attribute__((address_space(4))) HeadParams* kp =
         (const __attribute__((address_space(4))) HeadParams*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -1489,10 +1491,6 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
 
 template <int MODE, typename TT, int FLAGS = 0>
 hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char* name) {
-  // the epilogue's Markov and teacher loads take 32-bit offsets across a 256-row tile
-  constexpr int64_t kMaxLd = (int64_t)(0xffffffffLL - 1024) / 512;
-  if (p.markov && p.ldm > kMaxLd) return hipErrorInvalidValue;
-  if (StreamTail<MODE, TT, FLAGS>::kDmaU && !p.trows && p.ldt > kMaxLd) return hipErrorInvalidValue;
   static std::atomic<uint64_t> attr_done{0};
   if (const hipError_t e =
           ensure_dynamic_lds(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>), kHeadLdsBytes, attr_done))
