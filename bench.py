@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--stats-from", metavar="DIR", help="print a summary of a rocprofv3 --stats csv run")
     p.add_argument("--mfma-from", metavar="DIR",
                    help="print the matrix-core summary of one --pmc-driver pass with the MFMA counters")
+    p.add_argument("--memory-from", nargs="+", metavar="DIR",
+                   help="print the L1/L2 read-pipeline summary of the --pmc-driver passes with MEMORY_PASSES")
     p.add_argument("--command", default="", help="command line recorded in a printed summary")
     return p.parse_args()
 
@@ -300,6 +302,72 @@ def committed_mfma(config: str, kernel: str):
         return None
     return {"clock_GHz": float(m.group(1)), "mfma_busy": float(m.group(2)), "mfma_per_clock": float(m.group(3)),
             "mfma_source": os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))}
+
+
+# L1 -> L2 read pipeline counters, one --pmc pass each (with GRBM_GUI_ACTIVE and --kernel-trace)
+MEMORY_PASSES = (("TCP_TCC_READ_REQ_sum", "TCP_TCC_READ_REQ_LATENCY_sum", "TCP_PENDING_STALL_CYCLES_sum",
+                  "GRBM_GUI_ACTIVE"),
+                 ("TCC_HIT_sum", "TCC_MISS_sum", "GRBM_GUI_ACTIVE"))
+CUS = 256                           # MI355X compute units (one L1 each)
+
+
+def memory_summary(directories, config: str, command: str) -> str:
+    """Markdown: how each library GEMM kernel's loads move through the L1 (TCP) and the L2
+    (TCC), from the MEMORY_PASSES runs (per-dispatch medians, each pass's values taken
+    together):
+    * L1 -> L2 read requests per launch, one per 128-byte line;
+    * mean L2 read latency = TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ (cycles);
+    * lines in flight per CU = TCP_TCC_READ_REQ_LATENCY / (cycles x 256 CUs): the average
+      number of outstanding L1 misses per CU over the kernel (Little's law);
+    * L1 pending-stall share = TCP_PENDING_STALL_CYCLES / (cycles x 256 CUs);
+    * L2 hit rate = TCC_HIT / (TCC_HIT + TCC_MISS)."""
+    import statistics
+
+    per = {}
+    for directory in directories:
+        counters, durations = _per_dispatch(directory)
+        for d, (kname, vals) in counters.items():
+            name = timer_name(kname)
+            if not name or "GRBM_GUI_ACTIVE" not in vals or d not in durations:
+                continue
+            cycles = vals["GRBM_GUI_ACTIVE"] / 8.0
+            row = {}
+            if "TCP_TCC_READ_REQ_sum" in vals and vals["TCP_TCC_READ_REQ_sum"] > 0:
+                req, lat = vals["TCP_TCC_READ_REQ_sum"], vals["TCP_TCC_READ_REQ_LATENCY_sum"]
+                row.update(req=req, latency=lat / req, inflight=lat / (cycles * CUS),
+                           pending=vals["TCP_PENDING_STALL_CYCLES_sum"] / (cycles * CUS), cycles=cycles,
+                           ms=durations[d] / 1e6)
+            if "TCC_HIT_sum" in vals and vals["TCC_HIT_sum"] + vals["TCC_MISS_sum"] > 0:
+                row["hit"] = vals["TCC_HIT_sum"] / (vals["TCC_HIT_sum"] + vals["TCC_MISS_sum"])
+            for k, v in row.items():
+                per.setdefault(name, {}).setdefault(k, []).append(v)
+    if not per:
+        raise SystemExit(f"no library dispatches with memory counters in {directories}")
+    passes = "; ".join(f"`--pmc {' '.join(p)} --kernel-trace`" for p in MEMORY_PASSES)
+    out = [f"# L1 and L2 read pipeline per kernel: {config.upper()} (rocprofv3 TCP / TCC counters)", "",
+           "Commands (from the repository root on the MI355X box):", "", "```", command.strip(), "```", "",
+           f"One `bench.py --pmc-driver` pass per counter set ({passes}); per-dispatch medians. A request is one "
+           "128-byte line from a CU's L1 (TCP) to the L2 (TCC). Latency = TCP_TCC_READ_REQ_LATENCY / "
+           "TCP_TCC_READ_REQ, in cycles. Lines in flight per CU = TCP_TCC_READ_REQ_LATENCY / (cycles x 256 CUs), "
+           "the mean number of outstanding L1 misses per CU (Little's law). Pending stall = "
+           "TCP_PENDING_STALL_CYCLES / (cycles x 256 CUs). Cycles = GRBM_GUI_ACTIVE / 8 XCDs.", "",
+           "| kernel | duration ms | L1->L2 requests (M) | GB at 128 B | mean L2 latency (cycles) | "
+           "lines in flight per CU | L1 pending-stall share | L2 hit rate |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    machine = []
+
+    def med(vals, k):
+        return statistics.median(vals[k]) if k in vals else float("nan")
+
+    for name in sorted(per):
+        v = per[name]
+        out.append(f"| `{name}` | {med(v, 'ms'):.3f} | {med(v, 'req') / 1e6:.1f} | {med(v, 'req') * 128 / 1e9:.2f} | "
+                   f"{med(v, 'latency'):.0f} | {med(v, 'inflight'):.1f} | {med(v, 'pending'):.3f} | "
+                   f"{med(v, 'hit'):.3f} |")
+        machine.append(f"memory {name} requests={med(v, 'req'):.0f} latency={med(v, 'latency'):.1f} "
+                       f"inflight={med(v, 'inflight'):.2f} hit={med(v, 'hit'):.4f}")
+    out += ["", "Machine-readable:", "", "```"] + machine + ["```", ""]
+    return "\n".join(out)
 
 
 # --------------------------------------------------------------------------- CPU baseline
@@ -794,6 +862,9 @@ def main():
         return
     if args.mfma_from:
         print(mfma_summary(args.mfma_from, args.config, args.command))
+        return
+    if args.memory_from:
+        print(memory_summary(args.memory_from, args.config, args.command))
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
