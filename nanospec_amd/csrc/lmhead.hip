@@ -423,10 +423,13 @@ __device__ __forceinline__ bool gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
 // A row-major (K contiguous), B row-major [K, cols].  Both operands go global -> LDS
 // without registers, as in gemm_nt; B fragments use transposed LDS reads.  Per stage t:
 //   steps 0-2: the next step's 12 fragment reads (4 A, 8 B halves), one per MFMA;
-//   step 0: the B fills of stage t + 1 in the first eight MFMA slots;
+//   step 0: the B fills of stage t + 1 in the even MFMA slots;
 //   step 3: fill_barrier first (as in gemm_nt_tiles), then in its first eight slots stage
-//           t + 1's step-0 fragments and the A fills of stage t + 2.
-// Ends with a barrier.  KT >= 1.
+//           t + 1's step-0 fragments, and the A fills of stage t + 2 in the odd slots.
+// Every other slot rather than eight in a row keeps a CU's line misses in flight below
+// what its L1 queues (2% off the dh GEMM at C2).  Spreading further, over three steps as
+// gemm_nt_tiles does, measured 7% slower here; so did fills after the fragment reads
+// (slots 8-15).  Ends with a barrier.  KT >= 1.
 __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
                                             int64_t a0, int64_t amax, const uint16_t* __restrict__ B,
                                             int64_t ldb, int64_t c0, int64_t cmax, int64_t k0, int KT,
@@ -488,7 +491,7 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
           acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][q], tr_join(fb[cb][j]), acc[q][j], 0, 0, 0);
           __builtin_amdgcn_sched_barrier(0);
           if (kk < 3 && sl < 12) read_op(cb ^ 1, cur, kk + 1, sl);
-          if (kk == 0 && sl < 8) tb.issue(pb + t1 * ldb_stage, nxt + kStageBytes, wv, sl);
+          if (kk == 0 && !(sl & 1)) tb.issue(pb + t1 * ldb_stage, nxt + kStageBytes, wv, sl >> 1);
           if (kk == 3 && sl < 8) {
             const int u = sl;
             if (u < 4) {
@@ -497,8 +500,8 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
             } else {
               read_op(0, nxt, 0, 4 + u);
             }
-            ta.issue(pa + t2 * BK * 2, buf(t), wv, u);
           }
+          if (kk == 3 && (sl & 1)) ta.issue(pa + t2 * BK * 2, buf(t), wv, sl >> 1);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
