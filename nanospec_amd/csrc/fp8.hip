@@ -44,9 +44,11 @@ __device__ __forceinline__ float clamp448(float q) { return q != q ? q : fminf(f
 // the reference's tensor ops: a NaN makes the block's amax, so its scale and every code,
 // NaN; an infinity makes the scale inf, the finite entries' codes +-0 and its own code NaN
 // (inf / inf).  Either way the block dequantises to NaN and so do the row's logits.
+// Scale of (row, block kb) at xs[row * xs_row + kb * xs_blk]: [N, d/128] for callers,
+// [d/128, N] (contiguous over rows within a block) for the fp8 head.
 __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t n,
                                                         int64_t d, uint8_t* __restrict__ q,
-                                                        float* __restrict__ xs) {
+                                                        float* __restrict__ xs, int64_t xs_row, int64_t xs_blk) {
   const int64_t nb = d / kQBlock;
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= n * nb) return;
@@ -66,12 +68,12 @@ __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restri
   const float q1 = clamp448(__fdiv_rn(x1, den));
   const uint16_t codes = (uint16_t)(e4m3_code(q0) | (e4m3_code(q1) << 8));
   *reinterpret_cast<uint16_t*>(q + row * d + kb * kQBlock + 2 * lane) = codes;
-  if (lane == 0) xs[row * nb + kb] = s;
+  if (lane == 0) xs[row * xs_row + kb * xs_blk] = s;
 }
 
 struct Fp8Params {
   const uint8_t* qx;       // [N, d] e4m3 codes (row stride d)
-  const float* xs;         // [N, d/128]
+  const float* xs;         // [d/128, N]: each 128-K block's scales, contiguous over tokens
   const uint8_t* wq;       // [V, d] e4m3 codes
   const float* ws;         // [V/128, d/128]
   int64_t ldw;
@@ -191,11 +193,15 @@ void fp8_head_kernel(Fp8Params p) {
   DmaTile<FN, kWaves> tb;
   tb.init(p.d, t0, p.n, wv);
   const char* pb = reinterpret_cast<const char*>(p.qx + t0 * p.d);
-  uint32_t xsoff[2];   // this lane's two tokens' rows of xs (element offsets; N * d/128 < 2^31)
+  // this lane's two tokens (rows past N re-read the last); a block's scales are
+  // contiguous over tokens, so the 32 tokens of a load share one 128-byte line (from the
+  // callers' [N, d/128] layout a load touched 32 lines, which the fills evict from the
+  // L1: about 390 extra L2 requests per CU per stage, 7% of the kernel's time at C4)
+  uint32_t xsoff[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t t = t0 + wn * 64 + j * 32 + r;
-    xsoff[j] = (uint32_t)((t < p.n ? t : p.n - 1) * KB);
+    xsoff[j] = (uint32_t)(t < p.n ? t : p.n - 1);
   }
   lds_f32* lse_st = reinterpret_cast<lds_f32*>(lds + kLseOff);
   if (p.part && tid < FN) {   // first read after the first tile's barriers
@@ -284,8 +290,9 @@ void fp8_head_kernel(Fp8Params p) {
             asm volatile("" : "+v"(part[j]));   // keep the MFMAs in program order
             __builtin_amdgcn_sched_barrier(0);
             if (s == 0) {   // next stage's scales (complete by this stage's barrier)
-              xn[0] = p.xs[xsoff[0] + kn];
-              xn[1] = p.xs[xsoff[1] + kn];
+              const float* xsb = p.xs + (int64_t)kn * p.n;
+              xn[0] = xsb[xsoff[0]];
+              xn[1] = xsb[xsoff[1]];
               wnx = wsrow[kn];
             }
             // block row q + 1's A fragment kk, after its last use by block (q, 1)
@@ -430,14 +437,23 @@ Fp8Plan fp8_plan(int64_t n, int64_t v) {
 
 }  // namespace
 
-hipError_t fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs,
-                             hipStream_t st) {
+namespace {
+
+hipError_t launch_quant(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs, int64_t xs_row,
+                        int64_t xs_blk, hipStream_t st) {
   const int64_t items = n * (d / kQBlock);
   if (items == 0) return hipSuccess;
   NS_TIMED("fp8_quant", st);
   hipLaunchKernelGGL(fp8_quant_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st,
-                     static_cast<const uint16_t*>(x), ldx, n, d, q, xs);
+                     static_cast<const uint16_t*>(x), ldx, n, d, q, xs, xs_row, xs_blk);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t fp8_quantize_rows(const void* x, int64_t ldx, int64_t n, int64_t d, uint8_t* q, float* xs,
+                             hipStream_t st) {
+  return launch_quant(x, ldx, n, d, q, xs, d / kQBlock, 1, st);
 }
 
 size_t fp8_workspace_bytes(int64_t n, int64_t v, int64_t d) {
@@ -454,7 +470,7 @@ hipError_t fp8_teacher_logits(const void* x, int64_t ldx, const uint8_t* wq, int
   RowPart* part = reinterpret_cast<RowPart*>(static_cast<char*>(ws) + align_up((size_t)n * d, 256) +
                                              align_up((size_t)n * (d / kQBlock) * sizeof(float), 256));
   {
-    hipError_t e = fp8_quantize_rows(x, ldx, n, d, qx, xs, st);
+    hipError_t e = launch_quant(x, ldx, n, d, qx, xs, 1, n, st);   // scales [d/128, N] for the head
     if (e != hipSuccess) return e;
   }
   Fp8Params p;
