@@ -110,8 +110,8 @@ static_assert(kFp8Lds <= 160 * 1024, "fp8 head LDS");
 // s_waitcnt vmcnt(0) lgkmcnt(0) (expcnt not waited): gfx9 encoding, vmcnt[3:0] in bits
 // 3:0, expcnt in 6:4, lgkmcnt in 11:8, vmcnt[5:4] in 15:14.
 constexpr int kWaitAll = 0 | (7 << 4);
-// vmcnt(8): everything but the last 8 vector-memory operations (the next stage's fills)
-constexpr int kWaitPrologue = 8 | (7 << 4) | (15 << 8);
+// vmcnt(4): everything but the last 4 vector-memory operations (stage 1's A fills)
+constexpr int kWaitPrologue = 4 | (7 << 4) | (15 << 8);
 
 __device__ __forceinline__ u32x4_t rd16(const lds_t* base, int row, int chunk) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(base + lds_off(row, chunk));
@@ -226,8 +226,9 @@ void fp8_head_kernel(Fp8Params p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[q][j][e] = 0.f;
 
-    // prologue: stage 0's scales, then the fills of stages 0 and 1; wait for stage 0 only
-    // (vector-memory operations complete in order)
+    // prologue: stage 0's scales, then the fills of stage 0 and stage 1's A fills (its B
+    // fills go out in stage 0); wait for stage 0 only (vector-memory operations complete
+    // in order)
     float c_cur[2], c_prev[2] = {0.f, 0.f}, xn[2], wnx;
     {
       const float w0 = wsrow[0];
@@ -241,8 +242,7 @@ void fp8_head_kernel(Fp8Params p) {
     for (int i = 0; i < DmaTile<FN, kWaves>::NI; ++i) tb.issue(pb, buf(0) + kAStage, wv, i);
 #pragma unroll
     for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa + k1, buf(1), wv, i);
-#pragma unroll
-    for (int i = 0; i < DmaTile<FN, kWaves>::NI; ++i) tb.issue(pb + k1, buf(1) + kAStage, wv, i);
+    static_assert(DmaTile<FM, kWaves>::NI == 4 && DmaTile<FN, kWaves>::NI == 4, "fill slots");
     wait_barrier<kWaitPrologue>();
 
     i32x8_t a[2];            // [kk]: block row q's A fragments, reloaded after their last use
@@ -295,6 +295,13 @@ void fp8_head_kernel(Fp8Params p) {
               xn[1] = xsb[xsoff[1]];
               wnx = wsrow[kn];
             }
+            // stage t + 1's B fills (activation codes), one per slot in slots 0-3 (the last
+            // stage re-reads itself into the idle buffer).  That half of buffer t + 1 was last
+            // read in slots 12-15 of stage t - 2, before the previous barrier; this stage's
+            // barrier waits for them.  Issued with stage t + 2's A fills, eight per wave in
+            // slots 12-15, a CU's 64 fills overfilled its L1's miss queue and stalled the
+            // waves' issue: 7% slower at C4.
+            if (q == 0) tb.issue(pb + (int64_t)kn * kQBlock, buf(t + 1) + kAStage, wv, s);
             // block row q + 1's A fragment kk, after its last use by block (q, 1)
             if (q < 3 && j == 1) a[kk] = rd32(cb, wm * 128 + (q + 1) * 32 + r, kk * 4 + kh * 2);
             if (s == 11) {  // stage t + 1 landed everywhere, every wave done reading stage t
@@ -302,15 +309,8 @@ void fp8_head_kernel(Fp8Params p) {
             }
             if (q == 3) {
               const int u = s - 12;   // 0..3
-              // stage t + 2's fills into stage t's buffer, two per slot
-              if (fill2) {
-#pragma unroll
-                for (int m = 0; m < 2; ++m) {
-                  const int o = 2 * u + m;   // 0..7
-                  if (o < DmaTile<FM, kWaves>::NI) ta.issue(pa + k2, db, wv, o);
-                  else tb.issue(pb + k2, db + kAStage, wv, o - DmaTile<FM, kWaves>::NI);
-                }
-              }
+              // stage t + 2's A fills (weight codes) into stage t's buffer, one per slot
+              if (fill2) ta.issue(pa + k2, db, wv, u);
               // stage t + 1's fragments, each right after its last use in this stage: B (j, kk)
               // in its own slot, A row 0 in the slots of block (3, 1)
               if (more) {
