@@ -294,11 +294,11 @@ __device__ __forceinline__ void vm_barrier() {
 // A stage's 16 fills per wave (f = 0..7: A blocks, 8..15: B blocks) go out one every
 // third slot across three steps: fills 0-5 of stage t + 2 in step 3 of stage t (slots
 // 0, 3, .., 15, into buffer t & 1 just freed), fills 6-10 of stage t + 1 in step 0
-// (slots 2, 5, .., 14) and 11-15 in step 1 (slots 1, 4, .., 13).  A CU keeps about 60-100
+// (slots 1, 4, .., 13) and 11-15 in step 1 (slots 0, 3, .., 12).  A CU keeps about 60-100
 // line misses in flight to the L2; eight fills in consecutive slots (four waves: 256
 // lines) filled that queue and stalled the waves' issue.  Spreading them over three steps
-// took 1.5-2.7% off each head pass; over all four, the fills of step 2 land after the
-// barrier wants them (4-6% slower).
+// took 1.5-2.7% off each head pass at C2 and 1.5-2.5% at C3; over all four, the fills of
+// step 2 land after the barrier wants them (4-6% slower).
 //
 // The last stages would fill stages past the end.  With `tail.on` and KT >= 2 the slots
 // of two of those fills issue the caller's next loads instead (the epilogue's first
@@ -370,7 +370,7 @@ __device__ __forceinline__ bool gemm_nt_tiles(f32x16_t (&acc)[4][4], const DmaTi
           const int sl = 4 * q + j;
           if (kk == 0 && q >= 2 && M == 2) tail.issue(sb, 1, (q - 2) * 4 + j, nxt);
           // fills 6-10 and 11-15 of stage t + 1
-          if (M != 2 && ((kk == 0 && sl % 3 == 2) || (kk == 1 && sl % 3 == 1))) {
+          if (M != 2 && ((kk == 0 && sl % 3 == 1) || (kk == 1 && sl % 3 == 0 && sl < 15))) {
             const int f = kk == 0 ? 6 + sl / 3 : 11 + sl / 3;
             if (f < 8) ta.issue(pa + k1, nxt, wv, f);
             else tb.issue(pb + k1, nxt + kStageBytes, wv, f - 8);
