@@ -294,11 +294,12 @@ __device__ __forceinline__ void vm_barrier() {
 // A stage's 16 fills per wave (f = 0..7: A blocks, 8..15: B blocks) go out one every
 // third slot across three steps: fills 0-5 of stage t + 2 in step 3 of stage t (slots
 // 0, 3, .., 15, into buffer t & 1 just freed), fills 6-10 of stage t + 1 in step 0
-// (slots 1, 4, .., 13) and 11-15 in step 1 (slots 0, 3, .., 12).  A CU keeps about 60-100
-// line misses in flight to the L2; eight fills in consecutive slots (four waves: 256
-// lines) filled that queue and stalled the waves' issue.  Spreading them over three steps
-// took 1.5-2.7% off each head pass at C2 and 1.5-2.5% at C3; over all four, the fills of
-// step 2 land after the barrier wants them (4-6% slower).
+// (slots 1, 4, .., 13) and 11-15 in step 1 (slots 0, 3, .., 12).  Eight fills in
+// consecutive slots (four waves: 256 lines) stalled each wave's issue behind its own
+// burst: the CU then averaged 60-62 line misses in flight to the L2, 74 with the spread
+// (TCP_TCC_READ_REQ_LATENCY over cycles).  Spreading them over three steps took 1.5-2.7%
+// off each head pass at C2 and 1.5-2.5% at C3; over all four, the fills of step 2 land
+// after the barrier wants them (4-6% slower).
 //
 // The last stages would fill stages past the end.  With `tail.on` and KT >= 2 the slots
 // of two of those fills issue the caller's next loads instead (the epilogue's first
