@@ -60,14 +60,19 @@ __device__ __forceinline__ void mma_kn(f32x16_t (&acc)[4][4], const KnFrags& f) 
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(f.a[i]), tr_join(f.b[j]), acc[i][j], 0, 0, 0);
 }
 
-// All four steps of one stage, fragments double-buffered across steps.
+// All four steps of one stage, fragments double-buffered across steps; mem(kk) issues
+// step kk's share of the next stage's fills.
+template <typename Mem>
 __device__ __forceinline__ void stage_kn(f32x16_t (&acc)[4][4], const lds_t* sa, const lds_t* sb,
-                                         const uint32_t (&ta)[4], const uint32_t (&tbv)[4]) {
+                                         const uint32_t (&ta)[4], const uint32_t (&tbv)[4], Mem&& mem) {
   KnFrags f[2];
   read_kn_frags(f[0], sa, sb, 0, ta, tbv);
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     if (kk < 3) read_kn_frags(f[(kk + 1) & 1], sa, sb, kk + 1, ta, tbv);
+    __builtin_amdgcn_sched_barrier(0);
+    mem(kk);
+    __builtin_amdgcn_sched_barrier(0);
     mma_kn(acc, f[kk & 1]);
   }
 }
@@ -139,14 +144,18 @@ void dw2_kernel(Dw2Params p) {
   }
   for (int t = 0; t < KTf; ++t) {
     fill_barrier();   // stage t landed; everyone is done with stage t - 1's buffer
-    if (t + 1 < KTf) {
+    // the next stage's 16 fills per wave, four before each step's MFMAs: all 16 at once
+    // stalled the waves behind their own burst of L2 misses (10% slower)
+    const bool more = t + 1 < KTf;
+    stage_kn(acc, buf(t), buf(t) + kStage, tra, trb, [&](int kk) {
+      if (more) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ta.issue(pa + (t + 1) * sa_bytes, buf(t + 1), wv, i);
-        tb.issue(pb + (t + 1) * sb_bytes, buf(t + 1) + kStage, wv, i);
+        for (int i = 2 * kk; i < 2 * kk + 2; ++i) {
+          ta.issue(pa + (t + 1) * sa_bytes, buf(t + 1), wv, i);
+          tb.issue(pb + (t + 1) * sb_bytes, buf(t + 1) + kStage, wv, i);
+        }
       }
-    }
-    stage_kn(acc, buf(t), buf(t) + kStage, tra, trb);
+    });
   }
   const int kvalid = (int)(p.n - (int64_t)KTf * TK);
   if (kvalid > 0) {
@@ -155,7 +164,7 @@ void dw2_kernel(Dw2Params p) {
     load_kn_tail(lds, p.dl + k0 * p.ldd, p.ldd, v0, p.v, kvalid);
     load_kn_tail(lds + kStage, p.e + k0 * p.r, p.r, c0, p.r, kvalid);
     __syncthreads();
-    stage_kn(acc, lds, lds + kStage, tra, trb);
+    stage_kn(acc, lds, lds + kStage, tra, trb, [](int) {});
   }
   const int lane = threadIdx.x & 63, h = lane >> 5;
 #pragma unroll
