@@ -23,12 +23,16 @@ namespace ns {
 constexpr int kStreamThreads = 256;
 // Vocab entries per workgroup.  Pass 1 (read-only) is fastest with long ranges: few
 // partials and one block reduction per 16K entries.  Pass 2 reads two streams and writes
-// one; it moves bytes fastest with one 16-byte vector per thread and many short
-// workgroups (2048 entries), measured on MI355X: 6.3 TB/s against 5.1 TB/s at 16K.
+// one; it moves bytes fastest with one or two 16-byte vectors per thread and many short
+// workgroups (3072 entries), five of them per CU: kEmitLds of (unused) LDS caps a CU at
+// five.  Measured on MI355X at C1 (4096 x 248320 bf16): 0.955-0.964 ms, against 1.00-1.01 ms
+// for 2048 entries at eight workgroups per CU, 1.05 ms for 3072 at eight and 1.01 ms at
+// four; 16K entries moved 5.1 TB/s against 6.3.
 constexpr int64_t kStatsElems = 16384;
 constexpr int kStatsMaxSplits = 64;
-constexpr int64_t kEmitElems = 2048;
+constexpr int64_t kEmitElems = 3072;
 constexpr int kEmitMaxSplits = 256;
+constexpr int kEmitLds = 28 * 1024;   // 160 KB of LDS per CU: five workgroups
 
 static int splits_for(int64_t v, int64_t elems, int max_splits) {
   int64_t s = (v + elems - 1) / elems;
@@ -435,11 +439,11 @@ static hipError_t emit_dispatch(const void* z, int64_t ldz, const void* u, int64
   dim3 grid((unsigned)(S * a.n));
   NS_TIMED(EMIT ? "stream_emit" : "stream_accept", st);
   if (vec)
-    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, true, EMIT, ACCEPT>), grid, dim3(kStreamThreads), 0,
+    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, true, EMIT, ACCEPT>), grid, dim3(kStreamThreads), kEmitLds,
                        st, zp, ldz, up, ldu, v, chunk, S, row_stats, a.labels, a.weights, a.c_ce, a.c_kl,
                        a.inv_acc, dp, ldd, parta);
   else
-    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, false, EMIT, ACCEPT>), grid, dim3(kStreamThreads), 0,
+    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, false, EMIT, ACCEPT>), grid, dim3(kStreamThreads), kEmitLds,
                        st, zp, ldz, up, ldu, v, chunk, S, row_stats, a.labels, a.weights, a.c_ce, a.c_kl,
                        a.inv_acc, dp, ldd, parta);
   return hipGetLastError();
