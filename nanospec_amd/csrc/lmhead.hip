@@ -867,6 +867,42 @@ struct StreamTail {
   __device__ __forceinline__ void load_part(const StreamBases& sb, int s, int ci, lds_t* slot) const {
     if ((ci & 1) == 0 || kDmaU) load(sb, s, ci & 1, ci >> 1, slot);
   }
+
+  // The epilogue's own loads (steps 1-3) from per-lane offsets set up once per tile, for
+  // tiles whose 256 rows all lie below N and whose teacher rows are the tile's own (or
+  // none): load i of a region reads base + off[i] + s * 32 rows, the step term as the
+  // instruction's scalar offset.  load() re-derives each address from the thread index,
+  // about 15 instructions a load, and with one wave per SIMD every instruction of the
+  // epilogue costs an issue slot.
+  struct Offsets {
+    uint32_t m[8], u[8];
+    int wv;
+  };
+  __device__ __forceinline__ static bool direct(const StreamBases& sb) { return sb.rlast >= BN - 1 && sb.umode != 1; }
+  __device__ __forceinline__ void offsets(const StreamBases& sb, Offsets& o) const {
+    const int lane = tid & 63;
+    o.wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int b = 8 * o.wv + i;
+      const int tk = (b >> 4) * 128 + 2 * (b & 15) + (lane >> 5);   // the lane's token in step 0
+      const int c = (lane & 31) ^ (2 * (b & 7) + (lane >> 5));
+      const uint32_t cc = (uint32_t)((8 * c < sb.vleft ? c : 0) * 16);
+      o.m[i] = (uint32_t)tk * sb.mld + cc;
+      o.u[i] = (uint32_t)tk * sb.uld + cc;
+      // held in registers for the epilogue, not re-derived at each use
+      asm volatile("" : "+v"(o.m[i]), "+v"(o.u[i]));
+    }
+  }
+  __device__ __forceinline__ void load_direct(const StreamBases& sb, const Offsets& o, int s, int ci,
+                                              lds_t* slot) const {
+    const int i = ci >> 1;
+    lds_t* dst = slot + (8 * o.wv + i) * 1024;
+    if ((ci & 1) == 0)
+      dma16(sb.mbase, o.m[i], dst, (uint32_t)(32 * s) * sb.mld);
+    else if (kDmaU)
+      dma16(sb.ubase, o.u[i], dst + kSlotU, (uint32_t)(32 * s) * sb.uld);
+  }
 };
 
 typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
@@ -879,7 +915,7 @@ typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
 // V % 8 == 0, so each 8-entry chunk is wholly inside or outside the vocabulary.
 // `pre`: step 0 was loaded by the GEMM's tail (otherwise the K loop ended with a full
 // barrier and it is loaded here).  Ends with every wave's LDS reads done.
-template <int MODE, typename TT, int FLAGS, bool FULL>
+template <int MODE, typename TT, int FLAGS, bool FULL, bool DIRECT>
 __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, const f32x16_t (&acc)[4][4],
                                               const StreamTail<MODE, TT, FLAGS>& st, int KT, bool pre) {
   using ST = StreamTail<MODE, TT, FLAGS>;
@@ -904,6 +940,9 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
   uint16_t* const out = MODE == MODE_STORE ? p.out : p.dl;
   const int64_t ldo = MODE == MODE_STORE ? p.ldo : p.ldd;
   const float nan = __builtin_nanf("");
+  const StreamBases sb = st.bases();
+  typename ST::Offsets so;
+  if (DIRECT) st.offsets(sb, so);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // this step's loads landed in every wave (after step 0, the previous step's eight row
@@ -930,12 +969,13 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
     lds_t* sl = slot(s);
     // load ci of the next step, issued between this step's chunks so that the wave never
     // waits on a full memory queue with work left (a step's loads at once stalled issue)
-    StreamBases sbn{};
-    if (s < 3) sbn = st.bases();
     auto next = [&](int ci) {
       if (s < 3) {
         __builtin_amdgcn_sched_barrier(0);
-        st.load_part(sbn, s + 1, ci, slot(s + 1));
+        if (DIRECT)
+          st.load_direct(sb, so, s + 1, ci, slot(s + 1));
+        else
+          st.load_part(sb, s + 1, ci, slot(s + 1));
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -1244,10 +1284,12 @@ void head_kernel(HeadParams p) {
       pre = gemm_nt_tiles(acc, ta, reinterpret_cast<const char*>(p.w2 + v0 * p.ldw2), tb,
                           reinterpret_cast<const char*>(p.w1), KT, lds, tail);
     }
-    if (v0 + BM <= p.v)
-      epilogue_tile<MODE, TT, FLAGS, true>(p, lds, acc, tail, KT, pre);
+    if (v0 + BM > p.v)
+      epilogue_tile<MODE, TT, FLAGS, false, false>(p, lds, acc, tail, KT, pre);
+    else if (StreamTail<MODE, TT, FLAGS>::direct(tail.bases()))
+      epilogue_tile<MODE, TT, FLAGS, true, true>(p, lds, acc, tail, KT, pre);
     else
-      epilogue_tile<MODE, TT, FLAGS, false>(p, lds, acc, tail, KT, pre);
+      epilogue_tile<MODE, TT, FLAGS, true, false>(p, lds, acc, tail, KT, pre);
   }
 
   if (MODE == MODE_STORE && !(FLAGS & kStoreLse)) return;

@@ -30,11 +30,12 @@ __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + 
 // FLAT-encoded LDS fill as able to complete out of order with LDS reads, so it waits
 // for every outstanding LDS read (lgkmcnt(0)) before any fragment use; with the buffer
 // form it waits only for the reads a fragment needs.  Same bytes, same LDS layout.
-__device__ __forceinline__ void dma16(const char* base, uint32_t voff, lds_t* dst) {
+// `soff`: a wave-uniform byte offset added to every lane's (the instruction's scalar offset).
+__device__ __forceinline__ void dma16(const char* base, uint32_t voff, lds_t* dst, uint32_t soff = 0) {
   // word 3: 32-bit data format, the raw-buffer setting for gfx9-family descriptors
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, -1, 0x00020000);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, reinterpret_cast<__attribute__((address_space(3))) void*>(dst), 16,
-                                           voff, 0, 0, 0);
+                                           voff, soff, 0, 0);
 }
 
 // A ROWS-row operand tile (128-byte rows) fetched straight into LDS (dma16).  Each of the
