@@ -873,12 +873,15 @@ struct StreamTail {
   // none): load i of a region reads base + off[i] + s * 32 rows, the step term as the
   // instruction's scalar offset.  load() re-derives each address from the thread index,
   // about 15 instructions a load, and with one wave per SIMD every instruction of the
-  // epilogue costs an issue slot.
+  // epilogue costs an issue slot.  Such a tile never reads teacher rows itself (tdirect
+  // implies gathered rows), so its epilogue has no global loads of its own.
   struct Offsets {
     uint32_t m[8], u[8];
     int wv;
   };
-  __device__ __forceinline__ static bool direct(const StreamBases& sb) { return sb.rlast >= BN - 1 && sb.umode != 1; }
+  __device__ __forceinline__ static bool direct(const StreamBases& sb) {
+    return sb.rlast >= BN - 1 && (kDmaU ? sb.umode == 0 : true);
+  }
   __device__ __forceinline__ void offsets(const StreamBases& sb, Offsets& o) const {
     const int lane = tid & 63;
     o.wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -943,6 +946,10 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
   const StreamBases sb = st.bases();
   typename ST::Offsets so;
   if (DIRECT) st.offsets(sb, so);
+  // teacher rows read here rather than through LDS (never on a direct tile: the compiler then
+  // sees no global loads feeding the teacher values, and waits on none of the stream loads
+  // or row stores in flight)
+  const bool tdirect = !DIRECT && p.tdirect;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // this step's loads landed in every wave (after step 0, the previous step's eight row
@@ -995,7 +1002,7 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
       lzl = cr[0]; lul = cr[1]; cp = cr[2]; ct = cr[3];
     }
     const TT* urow = nullptr;
-    if (kReadU && (!kDmaU || p.tdirect)) {
+    if (kReadU && (!kDmaU || tdirect)) {
       const int trw = reinterpret_cast<const __attribute__((address_space(3))) int*>(lds + kTrowOff)[tk];
       urow = static_cast<const TT*>(p.teacher) + (int64_t)trw * p.ldt + v0;
     }
@@ -1022,7 +1029,7 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
         mraw[c] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2v_t*>(sl + off[c]);
       }
       if (kDmaU) {
-        if (p.tdirect) {
+        if (tdirect) {
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
             const int vl = wm * 128 + 8 * (8 * hs + c) + 4 * h;
@@ -1156,7 +1163,7 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
         if (mine) {
           const int k = (int)((yr >> 3) & 15);
           const int a = lb - 8 * h + ((k ^ (r & 15)) << 4) + 2 * (int)(yr & 7);
-          const float uy = kDmaU && !p.tdirect
+          const float uy = kDmaU && !tdirect
                                ? bf16_to_f32(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
                                      sl + kSlotU + a))
                                : load1(urow + yr);
