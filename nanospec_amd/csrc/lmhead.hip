@@ -946,10 +946,13 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
   const StreamBases sb = st.bases();
   typename ST::Offsets so;
   if (DIRECT) st.offsets(sb, so);
-  // teacher rows read here rather than through LDS (never on a direct tile: the compiler then
-  // sees no global loads feeding the teacher values, and waits on none of the stream loads
-  // or row stores in flight)
-  const bool tdirect = !DIRECT && p.tdirect;
+  // Teacher rows read here rather than through LDS.  A direct tile never takes that path (it
+  // implies gathered rows), and pass 1 drops it there: the compiler then sees no global loads
+  // feeding the teacher values and no longer waits, in each step's second half, for the
+  // stream loads the first half issued (0.8% off pass 1).  Pass 2 keeps the runtime test and
+  // with it those waits and one for the previous step's row stores; dropping it there was
+  // 0-1.5% slower (two boxes, C2 and C3).
+  const bool tdirect = (MODE == MODE_STATS && DIRECT) ? false : p.tdirect;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // this step's loads landed in every wave (after step 0, the previous step's eight row
