@@ -82,6 +82,7 @@ KERNEL_NAMES = [
     (r"lse_merge_kernel", "lse_merge"),
     (r"merge_kernel", "merge_rows"),
     (r"finalize_kernel", "finalize_metrics"),
+    (r"row_parts_kernel", "row_parts"),
     (r"accept_rows_kernel", "accept_rows"),
     (r"sum_partials_kernel", "dprev_reduce"),
     (r"gather_rows_kernel", "markov_gather"),
