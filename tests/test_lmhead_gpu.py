@@ -112,6 +112,8 @@ def test_c0_full_oracle(gpu_lib):
     (264, 192, 2056),    # two token tiles, one vocab tile plus a sliver
     (512, 64, 16384),    # several vocab splits
     (3072, 128, 16384),  # 12 token tiles: 64 splits in three rounds of 4 x 8 XCD blocks
+    (520, 128, 4104),    # two whole token tiles and one of 8 rows; a last vocab tile of 8 entries
+    (768, 64, 8200),     # whole token tiles only, each with a last vocab tile of 8 entries
 ])
 def test_odd_shapes(gpu_lib, n, d, v):
     hidden, weight, markov, teacher, slots = synthetic.head_inputs(n, d, v, 77 + n, DEV)
