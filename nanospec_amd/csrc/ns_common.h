@@ -42,6 +42,17 @@ __device__ __forceinline__ float min_nonneg(float a, float b) {
   return __uint_as_float(x < y ? x : y);
 }
 
+// The accept rate of a row, sum_v min(p_v, t_v), as torch.minimum(...).sum(-1) forms it
+// (objective.py:42): NaN when any p_v or t_v is NaN.  softmax(x) holds a NaN exactly when x
+// holds a NaN or a +inf or is -inf everywhere, and in each of those cases, and only then,
+// the row's online log-normaliser is NaN or -inf (a NaN or +inf term makes the running sum
+// NaN; an all -inf row leaves it 0).  So the per-entry sums may use min_nonneg, and the
+// row's sum is replaced by NaN when either log-normaliser is not finite.
+__device__ __forceinline__ float accept_rate_of(float sum, float lse_z, float lse_u) {
+  const bool ok = __builtin_fabsf(lse_z) <= 3.402823466e+38f && __builtin_fabsf(lse_u) <= 3.402823466e+38f;
+  return ok ? sum : __builtin_nanf("");
+}
+
 // ---- 8-element vector loads / stores (16 B for bf16, 32 B for f32) -----------
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {

@@ -311,7 +311,8 @@ __global__ __launch_bounds__(256) void accept_rows_kernel(const float* __restric
   float a = 0.f;
   for (int s = lane; s < splits; s += 64) a += p[s];
   a = wave_sum(a);
-  if (lane == 0) row_stats[r * kRowStatWidth + kAccept] = a;
+  float* rs = row_stats + r * kRowStatWidth;
+  if (lane == 0) rs[kAccept] = accept_rate_of(a, rs[kLseZ], rs[kLseU]);
 }
 
 static hipError_t launch_accept_rows(const float* parta, int splits, int64_t n, float* row_stats, hipStream_t st) {
@@ -337,7 +338,7 @@ __global__ __launch_bounds__(256) void row_parts_kernel(const float* __restrict_
   float a = p[0];
   for (int s = 1; s < splits; ++s) a += p[s];
   float* rs = row_stats + r * kRowStatWidth;
-  rs[kAccept] = a;
+  rs[kAccept] = accept_rate_of(a, rs[kLseZ], rs[kLseU]);
   if (partk != nullptr) {
     const float* q = partk + r * splits;
     float k = q[0];
@@ -361,7 +362,8 @@ __global__ __launch_bounds__(kFinalThreads) void finalize_kernel(int64_t n, int6
       const int64_t r = b * k + j;
       const float* rs = row_stats + r * kRowStatWidth;
       const bool vr = valid[r] != 0;
-      prod *= vr ? (double)rs[kAccept] : 0.0;
+      // (accept_rate * valid).cumprod(-1): a masked slot's NaN rate still poisons the block
+      prod *= (double)rs[kAccept] * (vr ? 1.0 : 0.0);
       len += prod;
       any = any || vr;
       const double w = weights[r];
@@ -369,10 +371,9 @@ __global__ __launch_bounds__(kFinalThreads) void finalize_kernel(int64_t n, int6
       ce += w * (double)rs[kCE];
       kl += w * (double)rs[kKL];
     }
-    if (any) {
-      asum += len;
-      atot += 1.0;
-    }
+    // (lengths * block_valid).sum(): a NaN length counts even in a block with no valid slot
+    asum += len * (any ? 1.0 : 0.0);
+    if (any) atot += 1.0;
   }
   __shared__ double sh[5][kFinalThreads / 64];
   double vals[5] = {den, ce, kl, asum, atot};

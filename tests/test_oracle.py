@@ -120,6 +120,68 @@ def test_acceptance_brute_force_random():
     assert ref.acceptance_length_counts(a, valid) == pytest.approx(_brute_accept(a, valid), rel=1e-14)
 
 
+def _torch_objective(z, u, w, y, valid, c_ce, c_kl):
+    """torch's evaluation (fp64) of the forward objective as objective.py:42-46 and 53-60
+    form it: torch.minimum, cumprod of accept_rate * valid, lengths * block_valid, and the
+    weighted sums.  Its NaN and inf semantics (softmax of an inf, 0 * inf, minimum with a
+    NaN) are torch's own."""
+    k = valid.shape[-1]
+    zt, ut = torch.from_numpy(z), torch.from_numpy(u)
+    wt, vt = torch.from_numpy(w.reshape(-1).astype(np.float64)), torch.from_numpy(valid)
+    ce = F.cross_entropy(zt, torch.from_numpy(y.reshape(-1)), reduction="none")
+    probs, target = zt.softmax(-1), ut.softmax(-1)
+    kl = (target * (ut.log_softmax(-1) - zt.log_softmax(-1))).sum(-1)
+    accept = torch.minimum(probs, target).sum(-1)
+    prefix = (accept.view(-1, k) * vt).cumprod(-1)
+    block_valid = vt.any(-1)
+    den = wt.sum()
+    ce_s, kl_s = (ce * wt).sum(), (kl * wt).sum()
+    acc_sum = ((prefix.sum(-1) + 1.0) * block_valid).sum()
+    return dict(ce=float(ce_s / den.clamp_min(1e-6)), kl=float(kl_s / den.clamp_min(1e-6)),
+                numerator=float(c_ce * ce_s + c_kl * kl_s), denominator=float(den), accept_len_sum=float(acc_sum),
+                accept_len_total=float(block_valid.double().sum())), accept.numpy(), kl.numpy(), ce.numpy()
+
+
+@pytest.mark.parametrize("tensor", ["z", "u"])
+@pytest.mark.parametrize("value", [np.nan, np.inf, -np.inf])
+@pytest.mark.parametrize("where", ["entry", "label", "row"])
+@pytest.mark.parametrize("masked", [False, True])
+def test_non_finite_logits_match_torch(tensor, value, where, masked):
+    """A NaN, +inf or -inf logit in z or u, in a valid or a masked slot: the oracle's metrics
+    and per-row CE, KL and accept rate are NaN / inf exactly where torch's evaluation of the
+    reference's lines is, and equal elsewhere (a masked slot's NaN accept rate still poisons
+    accept_len_sum through cumprod(accept * valid))."""
+    n, v, k = 16, 97, 8
+    z, u = _logits(30, n, v), _logits(31, n, v, scale=3.0, peak=8.0)
+    y = np.random.default_rng(32).integers(0, v, n)
+    valid = np.ones((n // k, k), dtype=bool)
+    valid[1, 6] = False
+    row = 14 if masked else 5
+    valid[row // k, row % k] = not masked
+    w = ref.slot_weights(valid, 4.0)
+    x = z if tensor == "z" else u
+    if where == "row":
+        x[row] = value
+    elif where == "label":
+        x[row, y[row]] = value
+    else:
+        x[row, (y[row] + 7) % v] = value
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        m, rows = ref.ce_kl_loss(z, u, w, y.reshape(-1, k), valid, 0.1, 0.9)
+    want, accept, kl, ce = _torch_objective(z, u, w, y, valid, 0.1, 0.9)
+    for key, val in want.items():
+        if math.isnan(val):
+            assert math.isnan(m[key]), key
+        else:
+            assert m[key] == pytest.approx(val, rel=1e-12), key
+    for got, lib in ((rows["accept_rate"], accept), (rows["kl"], kl), (rows["ce"], ce)):
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(lib))
+        fin = np.isfinite(lib)
+        np.testing.assert_array_equal(np.isfinite(got), fin)
+        np.testing.assert_array_equal(got[~fin & ~np.isnan(lib)], lib[~fin & ~np.isnan(lib)])
+        np.testing.assert_allclose(got[fin], lib[fin], rtol=1e-12, atol=1e-12)
+
+
 def test_empty_batch_metrics():
     v, k = 16, 4
     z = np.zeros((2 * k, v))
