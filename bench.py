@@ -9,7 +9,7 @@ input that is already resident in HBM.
     python bench.py [--steps K] [--warmup W] [--config c1|c2|c2x|c3|c4]
 
 Prints ONE JSON line.  By default the headline is C2 (the configuration the metric is
-quoted on) and C1 and C4 follow in the same process under "secondary".  One GPU only: ``--gpus N`` with N > 1 exits with a
+quoted on) and C1, C3, C4 and C2X follow in the same process under "secondary".  One GPU only: ``--gpus N`` with N > 1 exits with a
 message (the path is data-parallel over slots; the library has no collectives).
 """
 
@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c4", "c2x"],
-                   help="one workload alone; default: C2 (the headline) and then C1 and C4 as secondary lines")
+                   help="one workload alone; default: C2 (the headline), then C1, C3, C4 and C2X as secondary lines")
     p.add_argument("--no-secondary", action="store_true", help="default run: C2 only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--markov-skew", type=float, default=0.0,
@@ -597,8 +597,11 @@ def workload_head(device, args, which):
         ht = hidden.t().contiguous()   # a contiguous right operand (no transposed view)
         mm = _time_ms(lambda: torch.mm(weight, ht))
         del ht
-        return {"method": "torch.mm(W_lm, hidden^T) (hipBLASLt), bf16, random operands", "gemm_ms": mm,
-                "gemm_TFLOPs": gemm / (mm / 1e3) / 1e12}
+        out = {"method": "torch.mm(W_lm, hidden^T) (hipBLASLt), bf16, random operands", "gemm_ms": mm,
+               "gemm_TFLOPs": gemm / (mm / 1e3) / 1e12}
+        if fp8 is not None:
+            out["fp8"] = fp8_ceilings(fp8)
+        return out
 
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d, kernel_bytes=kernel_bytes,
                 kernel_flops=kernel_flops, kernel_fp8_flops=kernel_fp8_flops, cpu_baseline=cpu_baseline,
@@ -731,6 +734,39 @@ def sample_sha256(t) -> str:
     if sample.dtype == torch.bool:
         sample = sample.to(torch.uint8)
     return hashlib.sha256(sample.view(torch.uint8).numpy().tobytes()).hexdigest()[:16]
+
+
+def fp8_ceilings(fp8) -> dict:
+    """The vendor library's fp8 GEMM of the teacher head's shape (torch._scaled_mm, hipBLASLt):
+    x [N, d] e4m3 . W^T with W the same e4m3 codes [V, d], bf16 out.  Tensor-wise scales (a
+    plain fp8 GEMM, no block scales), and the 1x128 / 128x128 block scales of ops.fp8_linear
+    (ops.py:189-199) where the library takes them.  A form the library refuses is recorded
+    with its error instead of a time."""
+    import torch
+
+    xt, codes, scale = fp8
+    n, d = xt.shape
+    v = codes.shape[0]
+    flops = 2.0 * n * v * d
+    a = xt.float().clamp(-448, 448).to(torch.float8_e4m3fn)
+    b = codes.view(torch.float8_e4m3fn).t()          # [d, V], column-major as _scaled_mm wants
+    one = torch.ones((), dtype=torch.float32, device=xt.device)
+    forms = {
+        "tensorwise": lambda: torch._scaled_mm(a, b, scale_a=one, scale_b=one, out_dtype=torch.bfloat16),
+        "blockwise_1x128_128x128": lambda: torch._scaled_mm(
+            a, b, scale_a=torch.ones((n, d // 128), dtype=torch.float32, device=xt.device),
+            scale_b=scale.t(), out_dtype=torch.bfloat16),
+    }
+    out = {"method": "torch._scaled_mm(x_e4m3, W_e4m3^T) (hipBLASLt), bf16 out"}
+    for name, fn in forms.items():
+        try:
+            ms = _time_ms(fn)
+            out[name] = {"gemm_ms": ms, "gemm_TFLOPs": flops / (ms / 1e3) / 1e12,
+                         "frac_fp8_peak": flops / (ms / 1e3) / 1e12 / FP8_PEAK_TFLOPS}
+        except (RuntimeError, NotImplementedError, TypeError, ValueError) as e:
+            out[name] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:240]}"}
+    del a
+    return out
 
 
 def _time_ms(fn, reps: int = 5) -> float:
@@ -901,13 +937,16 @@ def main():
     del wl
     torch.cuda.empty_cache()
 
-    # the other configurations whose targets the north star names, in the same process:
-    # C1 (the logit stream against HBM) and C4 (the fp8 teacher head); each its own steps
+    # the other configurations, in the same process, each with its own warmup and steps: C1
+    # (the logit stream against HBM), C3 (the long batch), C4 (the fp8 teacher head) and C2X
+    # (C2 with final_norm, the factored Markov head and the pooled tail)
     secondary = {}
     if args.config is None and not args.no_secondary:
-        for name in ("c1", "c4"):
+        for name in ("c1", "c3", "c4", "c2x"):
             wl2 = WORKLOADS[name](device, args)
             r2 = measure(wl2, args, name)
+            if "ceilings" in wl2:
+                r2["library_ceilings"] = wl2["ceilings"]()
             r2["inputs_sha256"] = {k: sample_sha256(t) for k, t in wl2.get("inputs", {}).items() if t is not None}
             secondary[name] = r2
             del wl2

@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 5
+#define NS_ABI_VERSION 6
 
 #define NS_BF16 0
 #define NS_F32 1
@@ -147,6 +147,14 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
  * 10.6 MB at N = 32768 for V = 248,320); larger n * V is refused with NS_EWORKSPACE.
  * Nothing in the scratch has to start at zero.  Every call on one GPU shares that GPU's
  * array, so calls that overlap on one GPU (two streams, two threads) race; serialise them. */
+/* Per-device set-up of ns_lmhead_ce_kl_fwd_noalloc, for callers that capture it into a
+ * HIP graph: looks up the current device's static scratch (hipGetSymbolAddress) and raises
+ * the fused forward's kernels' dynamic-LDS limit (hipFuncSetAttribute), so that no call
+ * under capture makes either.  No counterpart in the reference.  Idempotent; call it once
+ * per device, with that device current, before the first capture.  Without it the first
+ * call on a device does the same. */
+int ns_device_init(void);
+
 int ns_lmhead_ce_kl_fwd_noalloc(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
                                 int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
                                 const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,

@@ -18,7 +18,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnanospec_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "nanospec_hip.h")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 NS_BF16, NS_F32 = 0, 1
 NS_WS_LOGITS, NS_WS_LMHEAD, NS_WS_LMHEAD_BWD, NS_WS_FP8 = 0, 1, 2, 3
 NS_WS_RMS_NORM_BWD, NS_WS_LMHEAD_NORM_BWD, NS_WS_TEACHER_LOGITS = 4, 5, 6
@@ -67,6 +67,7 @@ SIGNATURES = {
          _P, _I64, _P, _P, _P, _SZ, _P],
         _I,
     ),
+    "ns_device_init": ([], _I),
     "ns_lmhead_ce_kl_fwd_noalloc": (
         [_P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _TEACH, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F,
          _P, _I64, _P, _P, _P],

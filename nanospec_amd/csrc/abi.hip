@@ -266,6 +266,14 @@ int scratch_for_current_device(void** out) {
 
 extern "C" {
 
+int ns_device_init(void) {
+  void* ws = nullptr;
+  if (const int rc = scratch_for_current_device(&ws)) return rc;
+  if (const hipError_t e = ns::lmhead_forward_prepare(); e != hipSuccess)
+    return hip_status(e, "hipFuncSetAttribute (head kernels)");
+  return NS_OK;
+}
+
 int ns_lmhead_ce_kl_fwd_noalloc(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
                                 int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
                                 const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,

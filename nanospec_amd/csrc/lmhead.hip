@@ -38,6 +38,18 @@ constexpr int kThreads = 256;    // 4 waves as 2 (M) x 2 (N), 128 x 128 each
 constexpr int kStageBytes = BM * BK * 2;    // 32 KB per operand per stage
 constexpr int kGemmLds = 4 * kStageBytes;   // 2 stages x 2 operands = 128 KB
 
+// Wait states between the K loop's last v_mfma_f32_32x32x16_bf16 and the epilogue's
+// inline-asm v_accvgpr_read_b32 of its result, which the compiler's hazard tracking does
+// not see.  CDNA3/CDNA4 ask for (passes + 2) wait states between an XDL write and a VALU
+// read of the same register; the 32x32x16 bf16 form is taken at 16 passes (the count of
+// its 32x32x8 predecessor, an upper bound on gfx950).  Each s_nop 7 gives 8.  A change of
+// the K loop's MFMA must change kAccMfmaPasses with it.
+constexpr int kAccMfmaPasses = 16;
+constexpr int kAccReadWaitStates = kAccMfmaPasses + 2;
+constexpr int kAccReadNops = (kAccReadWaitStates + 7) / 8;
+static_assert(kAccReadNops * 8 >= kAccReadWaitStates, "too few s_nop 7 before the accumulator reads");
+static_assert(kAccReadNops == 3, "the epilogue's s_nop sequence below is written out for 3");
+
 
 
 // Per-lane byte offsets of a 256 (rows) x 64 (K) bf16 tile of a K-contiguous matrix,
@@ -961,8 +973,7 @@ __device__ __forceinline__ void epilogue_tile(const HeadParams& p, lds_t* lds, c
     if (s == 0) {
       vm_barrier<0>();
       // the K loop's last MFMAs may still be writing accumulators that the volatile reads
-      // below take without the compiler's hazard wait states: 24 wait states cover the
-      // 16-pass 32x32 MFMA's 18
+      // below take without the compiler's hazard wait states: kAccReadNops x 8 wait states
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     } else if (kOut && write) {
       vm_barrier<8>();
@@ -1558,12 +1569,16 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
   return pl;
 }
 
+// The dynamic-LDS limit of one head instantiation, raised once per device.
+template <int MODE, typename TT, int FLAGS = 0>
+hipError_t head_lds_attr() {
+  static std::atomic<uint64_t> attr_done{0};
+  return ensure_dynamic_lds(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>), kHeadLdsBytes, attr_done);
+}
+
 template <int MODE, typename TT, int FLAGS = 0>
 hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char* name) {
-  static std::atomic<uint64_t> attr_done{0};
-  if (const hipError_t e =
-          ensure_dynamic_lds(reinterpret_cast<const void*>(&head_kernel<MODE, TT, FLAGS>), kHeadLdsBytes, attr_done))
-    return e;
+  if (const hipError_t e = head_lds_attr<MODE, TT, FLAGS>()) return e;
   NS_TIMED(name, st);
   hipLaunchKernelGGL((head_kernel<MODE, TT, FLAGS>), dim3(grid), dim3(kThreads), kHeadLdsBytes, st, p);
   return hipGetLastError();
@@ -1583,6 +1598,16 @@ hipError_t head_forward_typed(HeadParams& p, const HeadPlan& pl, const SlotArgs&
 }
 
 }  // namespace
+
+hipError_t lmhead_forward_prepare() {
+  hipError_t e;
+  if ((e = head_lds_attr<MODE_STATS, uint16_t, 0>()) || (e = head_lds_attr<MODE_EMIT, uint16_t, 0>()) ||
+      (e = head_lds_attr<MODE_STATS, float, 0>()) || (e = head_lds_attr<MODE_EMIT, float, 0>()) ||
+      (e = head_lds_attr<MODE_STATS, uint16_t, kTeacherLse>()) || (e = head_lds_attr<MODE_EMIT, uint16_t, kTeacherLse>()) ||
+      (e = head_lds_attr<MODE_STATS, float, kTeacherLse>()) || (e = head_lds_attr<MODE_EMIT, float, kTeacherLse>()))
+    return e;
+  return hipSuccess;
+}
 
 size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d) {
   (void)d;

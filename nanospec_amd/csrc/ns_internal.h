@@ -83,6 +83,9 @@ struct MarkovFactors {
   int64_t ldw1, ldw2, r;
 };
 size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d);
+// Raises the dynamic-LDS limit of every head instantiation lmhead_forward can launch, on the
+// current device (done lazily at launch otherwise; this lets a caller do it before capture).
+hipError_t lmhead_forward_prepare();
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
                           const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
                           int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts,

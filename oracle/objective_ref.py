@@ -18,7 +18,11 @@ row_objective (accept a)   total-variation identity 1 - |p - t|_1 / 2;
 acceptance_length_counts   hand-computed known answers (all-invalid block,
                            truncation at a gap, a = 1, a = 0); brute force
 ce_kl_loss                 torch library loss (cross_entropy + kl_div);
-                           den = 0 clamp; empty batch -> accept_len 0
+                           den = 0 clamp; empty batch -> accept_len 0;
+                           NaN / inf logits against torch's evaluation of
+                           objective.py:42-46, 53-60
+metrics_from_rows          the tail of ce_kl_loss (same pins); chunked rows
+                           equal the whole batch's metrics
 ce_kl_backward             torch.autograd on the library loss; rows sum to 0;
                            w = 0 rows are 0; linear in 1/accumulation_steps
 lm_head_logits / dhidden   torch fp64 matmul; linearity
@@ -277,12 +281,22 @@ def ce_kl_loss(z, u, weights, labels, valid, c_ce=0.1, c_kl=0.9, dtype=np.float6
     else:
         for lo in range(0, n, chunk_rows):
             chunk(lo)
+    return metrics_from_rows(rows, weights, valid, c_ce, c_kl), rows
+
+
+def metrics_from_rows(rows, weights, valid, c_ce=0.1, c_kl=0.9) -> dict:
+    """The six LossMetrics plus ``loss`` and ``accept_len`` from per-row statistics (``rows``
+    with "ce", "kl" and "accept_rate" over all N rows, in row order), as objective.py:53-65
+    and 20-26 form them.  Rows may come from ``ce_kl_loss`` on chunks of the batch."""
+    valid = np.asarray(valid)
+    k = valid.shape[-1]
+    weights = np.asarray(weights, dtype=np.float64).reshape(-1)
     den = float(weights.sum())
-    ce_sum = float((rows["ce"] * weights).sum())
-    kl_sum = float((rows["kl"] * weights).sum())
+    ce_sum = float((np.asarray(rows["ce"], dtype=np.float64) * weights).sum())
+    kl_sum = float((np.asarray(rows["kl"], dtype=np.float64) * weights).sum())
     clamp = max(den, 1e-6)
     v2 = valid.reshape(-1, k)
-    acc_sum, acc_tot = acceptance_length_counts(rows["accept_rate"].reshape(v2.shape), v2)
+    acc_sum, acc_tot = acceptance_length_counts(np.asarray(rows["accept_rate"]).reshape(v2.shape), v2)
     metrics = dict(
         ce=ce_sum / clamp,
         kl=kl_sum / clamp,
@@ -293,7 +307,7 @@ def ce_kl_loss(z, u, weights, labels, valid, c_ce=0.1, c_kl=0.9, dtype=np.float6
     )
     metrics["loss"] = metrics["numerator"] / max(den, 1e-6)
     metrics["accept_len"] = acc_sum / max(acc_tot, 1.0)
-    return metrics, rows
+    return metrics
 
 
 def ce_kl_backward(z, u, weights, labels, c_ce=0.1, c_kl=0.9, accumulation_steps=1, dtype=np.float64):

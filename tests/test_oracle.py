@@ -182,6 +182,21 @@ def test_non_finite_logits_match_torch(tensor, value, where, masked):
         np.testing.assert_allclose(got[fin], lib[fin], rtol=1e-12, atol=1e-12)
 
 
+def test_metrics_from_chunked_rows_equal_the_whole_batch():
+    """Row statistics formed chunk by chunk give the whole batch's metrics (every row
+    statistic is row-local), bit for bit."""
+    n, v, k = 48, 301, 8
+    z, u = _logits(40, n, v), _logits(41, n, v, scale=3.0, peak=8.0)
+    y = np.random.default_rng(42).integers(0, v, n).reshape(-1, k)
+    valid = np.random.default_rng(43).uniform(size=(n // k, k)) > 0.2
+    w = ref.slot_weights(valid, 2.0)
+    m, rows = ref.ce_kl_loss(z, u, w, y, valid, 0.1, 0.9)
+    parts = [ref.ce_kl_loss(z[i:i + 16], u[i:i + 16], w[i // k:(i + 16) // k], y[i // k:(i + 16) // k],
+                            valid[i // k:(i + 16) // k], 0.1, 0.9)[1] for i in range(0, n, 16)]
+    joined = {key: np.concatenate([p[key] for p in parts]) for key in rows}
+    assert ref.metrics_from_rows(joined, w, valid, 0.1, 0.9) == m
+
+
 def test_empty_batch_metrics():
     v, k = 16, 4
     z = np.zeros((2 * k, v))

@@ -53,6 +53,38 @@ def test_noalloc_matches_the_workspace_entry_point(gpu_lib):
         assert bool(torch.isfinite(got[0]).all())
 
 
+def test_noalloc_under_graph_capture(gpu_lib):
+    """ns_device_init before capture, then ns_lmhead_ce_kl_fwd_noalloc captured with
+    torch.cuda.graph and replayed three times, with eager fills of the outputs and
+    synchronisations between the replays: every replay equals the workspace entry point's
+    result on the same inputs, bit for bit."""
+    lib = gpu_lib
+    assert lib.ns_device_init() == 0, lib.ns_last_error()
+    n, d, v = 512, 128, 8192
+    hidden, weight, markov, teacher, w, y, valid, k = _args(n, d, v, 33)
+    want = _call(lib, False, hidden, weight, markov, teacher, w, y, valid, k)
+    metrics = torch.empty(6, device=DEV)
+    row_stats = torch.empty((n, 8), device=DEV)
+    dl = torch.empty((n, v), dtype=torch.bfloat16, device=DEV)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    status = []
+    with torch.cuda.graph(graph):
+        status.append(lib.ns_lmhead_ce_kl_fwd_noalloc(
+            _lib.ptr(hidden), d, _lib.ptr(weight), d, _lib.ptr(markov), v, _lib.ptr(teacher), _lib.NS_BF16, v, None,
+            _lib.ptr(y), _lib.ptr(w), _lib.ptr(valid), n, d, v, k, 0.1, 0.9, 0.5, _lib.ptr(dl), v,
+            _lib.ptr(row_stats), _lib.ptr(metrics), _lib.stream(torch.device(DEV))))
+    _lib.check(status[0], "ns_lmhead_ce_kl_fwd_noalloc (captured)")
+    for rep in range(3):
+        for t in (metrics, row_stats, dl):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for g, w_ in zip((metrics, row_stats, dl), want):
+            assert torch.equal(g, w_), rep
+
+
 def test_noalloc_refuses_sizes_beyond_its_scratch(gpu_lib):
     n, d, v = 65536, 64, 248320
     status = gpu_lib.ns_lmhead_ce_kl_fwd_noalloc(
