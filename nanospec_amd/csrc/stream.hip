@@ -26,9 +26,10 @@ constexpr int kStreamThreads = 256;
 // 16K and 0.65 ms at 8K).  Pass 2 reads two streams and writes
 // one; it moves bytes fastest with one or two 16-byte vectors per thread and many short
 // workgroups (3072 entries), five of them per CU: kEmitLds of (unused) LDS caps a CU at
-// five.  Measured on MI355X at C1 (4096 x 248320 bf16): 0.955-0.964 ms, against 1.00-1.01 ms
-// for 2048 entries at eight workgroups per CU, 1.05 ms for 3072 at eight and 1.01 ms at
-// four; 16K entries moved 5.1 TB/s against 6.3.
+// five.  Measured on MI355X at C1 (4096 x 248320 bf16): 0.955-0.964 ms, against 1.00-1.01
+// ms for 2048 entries at eight workgroups per CU, 1.05 ms for 3072 at eight and 1.01 ms at
+// four; 16K entries moved 5.1 TB/s against 6.3.  The cap is for the pass that writes dl
+// only: the accept-only pass (no dl) runs 0.652 ms uncapped against 0.679 ms capped.
 constexpr int64_t kStatsElems = 32768;
 constexpr int kStatsMaxSplits = 64;
 constexpr int64_t kEmitElems = 3072;
@@ -451,11 +452,11 @@ static hipError_t emit_dispatch(const void* z, int64_t ldz, const void* u, int64
   dim3 grid((unsigned)(S * a.n));
   NS_TIMED(EMIT ? "stream_emit" : "stream_accept", st);
   if (vec)
-    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, true, EMIT, ACCEPT>), grid, dim3(kStreamThreads), kEmitLds,
+    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, true, EMIT, ACCEPT>), grid, dim3(kStreamThreads), EMIT ? kEmitLds : 0,
                        st, zp, ldz, up, ldu, v, chunk, S, row_stats, a.labels, a.weights, a.c_ce, a.c_kl,
                        a.inv_acc, dp, ldd, parta);
   else
-    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, false, EMIT, ACCEPT>), grid, dim3(kStreamThreads), kEmitLds,
+    hipLaunchKernelGGL((stream_emit_kernel<TZ, TU, TZ, false, EMIT, ACCEPT>), grid, dim3(kStreamThreads), EMIT ? kEmitLds : 0,
                        st, zp, ldz, up, ldu, v, chunk, S, row_stats, a.labels, a.weights, a.c_ce, a.c_kl,
                        a.inv_acc, dp, ldd, parta);
   return hipGetLastError();
