@@ -12,7 +12,11 @@
 //                     dl = (w/acc)[(c_ce + c_kl) p - c_kl t - c_ce e_y]
 //   finalize          one workgroup: accept rate per row, block prefix
 //                     lengths, the six LossMetrics scalars (fixed order).
+// bf16 rows of up to kRowCap entries take another route: stream_row_kernel, one workgroup
+// per row with the draft row kept on chip between its two phases (z read once, u twice),
+// then finalize.  fp32 logits, unaligned rows and longer rows take the split passes.
 // Every reduction has a fixed order, so results are bitwise reproducible.
+#include <atomic>
 #include <type_traits>
 
 #include "ns_internal.h"
@@ -415,6 +419,191 @@ hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, fl
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- one workgroup per row
+
+// bf16 z and u with V <= kRowCap: one workgroup per row keeps the draft row z on chip
+// between the statistics phase and the emit phase, so z is read once and u twice: 8 V bytes
+// per row with dl (6 V without), against 10 V (8 V) for stream_stats + stream_emit.
+// Thread t owns the row's 16-byte vectors q = i * kRowThreads + t, i = 0 .. kRowVec - 1:
+// the first kRowLdsVec in LDS (slot (i, t) at 16 (i kRowThreads + t), conflict-free), the
+// rest in registers.  Loads go out kRowGroup vectors at a time, before any is used.
+constexpr int kRowThreads = 512;
+constexpr int kRowLdsVec = 19;
+constexpr int kRowRegVec = 42;
+constexpr int kRowVec = kRowLdsVec + kRowRegVec;
+constexpr int64_t kRowCap = (int64_t)kRowVec * kRowThreads * 8;   // 249,856 entries
+constexpr int kRowLds = kRowLdsVec * kRowThreads * 16;             // 155,648 bytes
+constexpr int kRowGroup = 4;
+static_assert(kRowLds + 1024 <= 160 * 1024, "row kernel LDS");
+
+typedef uint32_t u32x4n_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void unpack8(const u32x4n_t& w, float* f) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = bf16_lo(w[e]);
+    f[2 * e + 1] = bf16_hi(w[e]);
+  }
+}
+
+template <bool EMIT>
+__global__ __launch_bounds__(kRowThreads) void stream_row_kernel(
+    const uint16_t* __restrict__ z, int64_t ldz, const uint16_t* __restrict__ u, int64_t ldu, int64_t v,
+    const int64_t* __restrict__ labels, const float* __restrict__ weights, float c_ce, float c_kl, float inv_acc,
+    uint16_t* __restrict__ dl, int64_t ldd, float* __restrict__ row_stats) {
+  extern __shared__ __attribute__((aligned(16))) char row_lds[];
+  __shared__ PairState red[kRowThreads / 64];
+  __shared__ float red_a[kRowThreads / 64];
+  __shared__ float zy_sh;
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  // each row through a buffer resource of its own length (accesses past it read 0 and
+  // store nothing); vector i of this thread at byte tid * 16 + i * kRowThreads * 16
+  const uint32_t row_bytes = (uint32_t)(v * 2);
+  const __amdgpu_buffer_rsrc_t zrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(z + r * ldz), 0, row_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t urs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(u + r * ldu), 0, row_bytes, 0x00020000);
+  const int voff = tid * 16;
+  const int nvec = (int)(v >> 3);
+  const int full = nvec / kRowThreads, rem = nvec % kRowThreads;   // vectors i < full exist in every thread
+  auto has = [&](int i) { return i < full || (i == full && tid < rem); };
+  auto slot = [&](int i) { return reinterpret_cast<u32x4n_t*>(row_lds + (i * kRowThreads + tid) * 16); };
+  const int64_t y = labels[r];
+  // phase 1: (max, sum-exp) of z and u and A = sum exp(u - m_u)(u - z); z kept on chip
+  u32x4n_t zreg[kRowRegVec];
+  PairState st = pair_init();
+  int soff = 0;
+#pragma unroll
+  for (int g = 0; g < kRowVec; g += kRowGroup) {
+    u32x4n_t zv[kRowGroup], uv[kRowGroup];
+#pragma unroll
+    for (int k = 0; k < kRowGroup; ++k) {
+      const int i = g + k;
+      if (i < kRowVec && has(i)) {
+        zv[k] = __builtin_amdgcn_raw_buffer_load_b128(zrs, voff, soff, 2);
+        uv[k] = __builtin_amdgcn_raw_buffer_load_b128(urs, voff, soff, 0);
+      }
+      soff += kRowThreads * 16;   // formed here, not hoisted into one SGPR per vector
+      asm volatile("" : "+s"(soff));
+    }
+#pragma unroll
+    for (int k = 0; k < kRowGroup; ++k) {
+      const int i = g + k;
+      if (i < kRowVec && has(i)) {
+        float zf[8], uf[8];
+        unpack8(zv[k], zf);
+        unpack8(uv[k], uf);
+        pair_update<8>(st, zf, uf);
+        const int q = i * kRowThreads + tid;
+        if ((y >> 3) == q) {   // this vector holds the label entry (y in [0, V)): one writer,
+                               // read after the barriers below; zy_sh is not read otherwise
+          float x = zf[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) x = (int)(y & 7) == e ? zf[e] : x;
+          zy_sh = x;
+        }
+        if (i < kRowLdsVec)
+          *slot(i) = zv[k];
+        else
+          zreg[i < kRowLdsVec ? 0 : i - kRowLdsVec] = zv[k];
+      }
+    }
+  }
+  st = wave_reduce(st);
+  if ((tid & 63) == 0) red[tid >> 6] = st;
+  __syncthreads();
+  st = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / 64; ++w) st = pair_merge(st, red[w]);
+  const float lz = st.mz + logf(st.sz);
+  const float lu = st.mu + logf(st.su);
+  // phase 2: p, t, sum min(p, t) and dl, z from chip, u read again
+  const float lzl = lz * kLog2e, lul = lu * kLog2e;
+  const float w = weights[r] * inv_acc;
+  const float cp = y == kIgnoreIndex ? w * c_kl : w * (c_ce + c_kl), ct = w * c_kl, cy = w * c_ce;
+  const __amdgpu_buffer_rsrc_t drs =
+      __builtin_amdgcn_make_buffer_rsrc(EMIT ? dl + r * ldd : nullptr, 0, EMIT ? row_bytes : 0, 0x00020000);
+  float acc = 0.f;
+  soff = 0;
+  int sout = 0;
+#pragma unroll
+  for (int g = 0; g < kRowVec; g += kRowGroup) {
+    u32x4n_t uv[kRowGroup];
+#pragma unroll
+    for (int k = 0; k < kRowGroup; ++k) {
+      const int i = g + k;
+      if (i < kRowVec && has(i)) uv[k] = __builtin_amdgcn_raw_buffer_load_b128(urs, voff, soff, 2);
+      soff += kRowThreads * 16;
+      asm volatile("" : "+s"(soff));
+    }
+#pragma unroll
+    for (int k = 0; k < kRowGroup; ++k) {
+      const int i = g + k;
+      if (i < kRowVec && has(i)) {
+        const u32x4n_t zv = i < kRowLdsVec ? *slot(i) : zreg[i < kRowLdsVec ? 0 : i - kRowLdsVec];
+        float zf[8], uf[8], d[8];
+        unpack8(zv, zf);
+        unpack8(uv[k], uf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pp = fast_exp2(__builtin_fmaf(zf[e], kLog2e, -lzl));
+          const float tt = fast_exp2(__builtin_fmaf(uf[e], kLog2e, -lul));
+          acc += min_nonneg(pp, tt);
+          d[e] = __builtin_fmaf(cp, pp, -ct * tt);
+        }
+        if (EMIT) {
+          const int64_t i0 = 8 * (int64_t)(i * kRowThreads + tid);
+          if ((uint64_t)(y - i0) < 8ull) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (i0 + e == y) d[e] -= cy;
+          }
+          const u32x4n_t o = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]), pack_bf16x2(d[4], d[5]),
+                              pack_bf16x2(d[6], d[7])};
+          __builtin_amdgcn_raw_buffer_store_b128(o, drs, voff, sout, 2);
+        }
+      }
+      sout += kRowThreads * 16;
+      asm volatile("" : "+s"(sout));
+    }
+  }
+  acc = wave_sum(acc);
+  if ((tid & 63) == 0) red_a[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    float a = red_a[0];
+#pragma unroll
+    for (int w2 = 1; w2 < kRowThreads / 64; ++w2) a += red_a[w2];
+    // CE and KL as merge_kernel forms them (labels outside [0, V) other than the ignore
+    // index make CE NaN)
+    const float yv = (y >= 0 && y < v) ? zy_sh : __builtin_nanf("");
+    float* o = row_stats + r * kRowStatWidth;
+    o[kLseZ] = lz;
+    o[kLseU] = lu;
+    o[kCE] = y == kIgnoreIndex ? lz - lz : lz - yv;
+    o[kKL] = st.A / st.su - lu + lz;
+    o[kAccept] = accept_rate_of(a, lz, lu);
+    o[kZy] = yv;
+    o[6] = 0.f;
+    o[7] = 0.f;
+  }
+}
+
+template <bool EMIT>
+static hipError_t launch_row(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v, const SlotArgs& a,
+                             void* dl, int64_t ldd, float* row_stats, hipStream_t st) {
+  static std::atomic<uint64_t> attr_done{0};
+  if (const hipError_t e =
+          ensure_dynamic_lds(reinterpret_cast<const void*>(&stream_row_kernel<EMIT>), kRowLds, attr_done))
+    return e;
+  NS_TIMED(EMIT ? "stream_row" : "stream_row_accept", st);
+  hipLaunchKernelGGL(stream_row_kernel<EMIT>, dim3((unsigned)a.n), dim3(kRowThreads), kRowLds, st,
+                     static_cast<const uint16_t*>(z), ldz, static_cast<const uint16_t*>(u), ldu, v, a.labels,
+                     a.weights, a.c_ce, a.c_kl, a.inv_acc, static_cast<uint16_t*>(dl), ldd, row_stats);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- host dispatch
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -466,6 +655,15 @@ template <typename TZ, typename TU>
 static hipError_t forward_typed(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v,
                                 const SlotArgs& a, void* dl, int64_t ldd, float* row_stats, float* metrics,
                                 void* ws, hipStream_t st) {
+  // bf16 rows that fit on chip, 16-byte aligned: one workgroup per row
+  if (std::is_same<TZ, uint16_t>::value && std::is_same<TU, uint16_t>::value && v % 8 == 0 && v <= kRowCap &&
+      aligned16(z) && aligned16(u) && ldz % 8 == 0 && ldu % 8 == 0 &&
+      (dl == nullptr || (aligned16(dl) && ldd % 8 == 0))) {
+    hipError_t e = dl != nullptr ? launch_row<true>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, st)
+                                 : launch_row<false>(z, ldz, u, ldu, v, a, nullptr, 0, row_stats, st);
+    if (e != hipSuccess) return e;
+    return launch_finalize(nullptr, 1, a, row_stats, metrics, st);   // accept rates already in row_stats
+  }
   StreamWs w;
   stream_ws_layout(a.n, v, ws, &w);
   const int S = stream_splits(a.n, v);

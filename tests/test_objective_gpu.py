@@ -99,6 +99,7 @@ def test_golden_vectors(gpu_lib):
     (64, 8192, torch.float32),
     (32, 1001, torch.bfloat16),      # odd V: unaligned rows -> scalar path
     (16, 40000, torch.bfloat16),     # several vocab splits with a ragged last split
+    (8, 250_008, torch.bfloat16),    # a bf16 row past the on-chip capacity (249,856): two passes
 ])
 def test_parity_small(gpu_lib, n, v, dtype):
     z, u, slots = synthetic.logits_inputs(n, v, 7 + n + v, DEV)
@@ -118,6 +119,27 @@ def test_parity_small(gpu_lib, n, v, dtype):
         _assert_dl_bf16(_np(dl).reshape(n, v), dl_ref)
     else:
         np.testing.assert_allclose(_np(dl).reshape(n, v), dl_ref, rtol=1e-4, atol=1e-8)
+
+
+@pytest.mark.parametrize("n,v", [(64, 8192), (24, 40000), (16, 248_320)])
+def test_row_resident_path_matches_the_two_pass_path(gpu_lib, n, v):
+    """bf16 rows within the on-chip capacity run one workgroup per row (z kept on chip);
+    the same values with an fp32 teacher run the two split passes.  Both restate
+    objective.py:49-80 with the same per-entry formulas: metrics within 2e-6 relative, row
+    statistics within fp32 summation-order error, dl equal except where an lse's last bit
+    moves one entry's rounding."""
+    z, u, slots = synthetic.logits_inputs(n, v, 300 + n, DEV)
+    o = Objective(block_size=8)
+    m_row, s_row, dl_row = _run(z, u, slots, o)
+    m_two, s_two, dl_two = _run(z, u.float(), slots, o)
+    for f in FIELDS:
+        a, b = float(getattr(m_row, f)), float(getattr(m_two, f))
+        assert a == pytest.approx(b, rel=2e-6, abs=1e-6), f
+    np.testing.assert_allclose(_np(s_row.row_stats)[:, :5], _np(s_two.row_stats)[:, :5], rtol=2e-6, atol=2e-5)
+    np.testing.assert_array_equal(_np(s_row.row_stats)[:, 5], _np(s_two.row_stats)[:, 5])
+    assert float((dl_row == dl_two).float().mean()) > 0.999
+    m_ref, _, _ = _oracle(z, u, slots, o)
+    _assert_metrics(_metrics(m_row), m_ref)
 
 
 def test_accumulation_steps_and_reemission(gpu_lib):
