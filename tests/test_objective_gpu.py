@@ -142,6 +142,32 @@ def test_row_resident_path_matches_the_two_pass_path(gpu_lib, n, v):
     _assert_metrics(_metrics(m_row), m_ref)
 
 
+@pytest.mark.parametrize("v", [8192, 40000])
+def test_label_pick_at_vector_and_row_edges(gpu_lib, v):
+    """Labels at the first and last entry of a row, at the edges of a 16-byte vector and in the
+    last, partly filled round of vectors of the row-resident kernel (V = 40000: 5000 vectors,
+    9 full rounds of 512 threads and 392 vectors in the tenth): z_label, CE and dl[y] exact
+    against the oracle's pick."""
+    n = 16
+    z, u, slots = synthetic.logits_inputs(n, v, 400 + v, DEV)
+    # vector q = 512 i + t holds entries 8q .. 8q + 7; the last full round ends at vector
+    # 512 * (nvec // 512) - 1
+    last_full = 8 * 512 * ((v // 8) // 512)
+    picks = [0, v - 1, 7, 8, v - 8, v - 9, last_full - 1, last_full - 8, last_full % v, (last_full + 8) % v,
+             8 * 511 + 7, 8 * 512, 1, 2, 3, 4]
+    y = torch.tensor(picks, dtype=torch.int64, device=DEV).view(-1, 8)
+    slots = synthetic.Slots(slots.weights, y, slots.valid)
+    o = Objective(block_size=8)
+    m, saved, dl = _run(z, u, slots, o)
+    m_ref, rows, dl_ref = _oracle(z, u, slots, o)
+    _assert_metrics(_metrics(m), m_ref)
+    rs = _np(saved.row_stats)
+    zy = _np(z)[np.arange(n), np.array(picks)]
+    np.testing.assert_array_equal(rs[:, 5], zy)
+    np.testing.assert_allclose(rs[:, 2], rows["ce"], rtol=2e-6, atol=2e-5)
+    _assert_dl_bf16(_np(dl).reshape(n, v), dl_ref)
+
+
 def test_accumulation_steps_and_reemission(gpu_lib):
     z, u, slots = synthetic.logits_inputs(32, 4096, 11, DEV)
     o = Objective(block_size=8)
