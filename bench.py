@@ -858,6 +858,10 @@ def measure(wl, args, config_name):
         roof["traffic"] = tr[0] if tr else None
         if tr:
             roof["traffic_source"] = tr[1]
+            # the bytes the kernel moves (counters), over this run's mean launch time: the
+            # executed HBM rate beside the algorithmic one above
+            roof["traffic_GBs"] = tr[0] / (k_ms / 1e3) / 1e9
+            roof["traffic_frac_hbm"] = roof["traffic_GBs"] / HBM_PEAK_GBS
         mf = committed_mfma(config_name, kernel)
         if mf:
             roof.update(mf)
