@@ -76,8 +76,9 @@ KERNEL_NAMES = [
     (r"dh_reduce_kernel", "dh_reduce"),
     (r"dh_kernel", "dh_gemm"),
     (r"stream_stats_kernel", "stream_stats"),
-    (r"stream_row_kernel<true>", "stream_row"),
-    (r"stream_row_kernel<false>", "stream_row_accept"),
+    (r"stream_group_kernel<[^,]+, [^,]+, true>", "stream_group"),
+    (r"stream_group_kernel<[^,]+, [^,]+, false>", "stream_group_accept"),
+    (r"group_clear_kernel", "group_clear"),
     # stream_emit_kernel<TZ, TU, TD, VEC, EMIT, ACCEPT>
     (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), true", "stream_emit"),
     (r"stream_emit_kernel<[^,]+, [^,]+, [^,]+, (?:true|false), false", "stream_accept"),
@@ -453,9 +454,9 @@ def workload_c1(device, args):
     kernel_bytes = {
         "stream_stats": 4 * v * n,   # read z, u
         "stream_emit": 6 * v * n,    # read z, u, write dl
-        # one workgroup per row, z kept on chip: the whole step's algorithmic bytes in one
-        # launch (it executes 8 V per row: z once, u twice, dl)
-        "stream_row": 6 * v * n,
+        # four workgroups per row, each keeping its quarter of z and u on chip: the whole
+        # step's algorithmic bytes in one launch, each byte moved once
+        "stream_group": 6 * v * n,
     }
 
     def cpu_baseline(rows):
@@ -498,7 +499,7 @@ def workload_c1(device, args):
                 "read2_write1_ms": rw, "read2_write1_GBs": 3 * b / (rw / 1e3) / 1e9}
 
     return dict(step=step, n=n, per_slot_bytes=per_slot, per_slot_flops=None, kernel_bytes=kernel_bytes,
-                kernel_flops={}, stream_kernels=("stream_stats", "stream_emit", "stream_row"), cpu_baseline=cpu_baseline,
+                kernel_flops={}, stream_kernels=("stream_stats", "stream_emit", "stream_group"), cpu_baseline=cpu_baseline,
                 config=config, dtype="bf16", ceilings=ceilings,
                 inputs={"draft_logits": z, "teacher_logits": u, "weights": slots.weights,
                         "target_ids": slots.target_ids, "valid": slots.valid})

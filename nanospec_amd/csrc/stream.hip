@@ -12,9 +12,10 @@
 //                     dl = (w/acc)[(c_ce + c_kl) p - c_kl t - c_ce e_y]
 //   finalize          one workgroup: accept rate per row, block prefix
 //                     lengths, the six LossMetrics scalars (fixed order).
-// bf16 rows of up to kRowCap entries take another route: stream_row_kernel, one workgroup
-// per row with the draft row kept on chip between its two phases (z read once, u twice),
-// then finalize.  fp32 logits, unaligned rows and longer rows take the split passes.
+// bf16 rows of up to kRowCap entries take another route: stream_group_kernel, two
+// workgroups per row, each keeping its half of z and u on chip between the statistics and
+// the emit phase (both read once), then finalize.  fp32 logits, unaligned rows and longer rows
+// take the split passes.
 // Every reduction has a fixed order, so results are bitwise reproducible.
 #include <atomic>
 #include <type_traits>
@@ -78,8 +79,6 @@ static size_t stream_ws_layout(int64_t n, int64_t v, void* base, StreamWs* out) 
   }
   return b1 + b2 + b3;
 }
-
-size_t stream_workspace_bytes(int64_t n, int64_t v) { return stream_ws_layout(n, v, nullptr, nullptr); }
 
 // Block-wide merge of pair states; thread 0 returns the result.
 __device__ __forceinline__ PairState block_reduce_pair(PairState st) {
@@ -419,24 +418,62 @@ hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, fl
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------- one workgroup per row
+// ---------------------------------------------------------------- a group of workgroups per row
 
-// bf16 z and u with V <= kRowCap: one workgroup per row keeps the draft row z on chip
-// between the statistics phase and the emit phase, so z is read once and u twice: 8 V bytes
-// per row with dl (6 V without), against 10 V (8 V) for stream_stats + stream_emit.
-// Thread t owns the row's 16-byte vectors q = i * kRowThreads + t, i = 0 .. kRowVec - 1:
-// the first kRowLdsVec in LDS (slot (i, t) at 16 (i kRowThreads + t), conflict-free), the
-// rest in registers.  Loads go out kRowGroup vectors at a time, before any is used.
-constexpr int kRowThreads = 512;
-constexpr int kRowLdsVec = 19;
-constexpr int kRowRegVec = 42;
-constexpr int kRowVec = kRowLdsVec + kRowRegVec;
-constexpr int64_t kRowCap = (int64_t)kRowVec * kRowThreads * 8;   // 249,856 entries
-constexpr int kRowLds = kRowLdsVec * kRowThreads * 16;             // 155,648 bytes
-constexpr int kRowGroup = 4;
-static_assert(kRowLds + 1024 <= 160 * 1024, "row kernel LDS");
+// bf16 z and u with V <= kRowCap: G workgroups of T threads share a row.  Member h keeps its
+// contiguous share of both z and u on chip between the statistics phase and the emit phase,
+// so each is read once: 6 V bytes per row with dl (4 V without), against 10 V (8 V) for
+// stream_stats + stream_emit.  Between the phases the members swap their partial statistics
+// (PairState and the label's logit) through the workspace and merge them in member order;
+// the last member of a row to finish sums the accept partials in member order and writes the
+// row's statistics.
+//
+// Workgroups take tickets from a counter: ticket t is member t % G of row t / G.  A member
+// waits only for members holding tickets, which have started and so finish phase 1 without
+// waiting, whatever order the workgroups are dispatched in.  An exchanged value is one
+// 64-bit word, tag << 32 | bits, written and read with relaxed device-scope atomics (coherent
+// across the XCDs' L2s): a word is complete once its tag is non-zero, so no fence orders it
+// against other words.  group_clear_kernel zeroes the counter and the words before each
+// launch.  Every wait is bounded (kGrpSpinLimit polls, seconds): one that runs out, which the
+// argument above rules out, yields NaN statistics instead of a hang.
+//
+// Storage of member h's share (16-byte vectors b .. b + cnt of the row, b = h ceil(nvec / G)):
+// thread t owns vectors b + i T + t.  Columns i < kGrpRegCols of z and u sit in registers,
+// filled by ordinary loads; columns kGrpRegCols + c, c < kGrpLdsCols, in LDS (z at slot
+// (c, t), u at slot (kGrpLdsCols + c, t), slot (k, t) at byte 16 (k T + t)), filled straight
+// from memory (buffer_load ... lds).  All of a share's loads are issued, unconditionally,
+// before any is used (vectors past the share read zeros through the buffer range and are
+// never folded): the register columns first, which phase 1 then consumes in issue order while
+// the rest land.  Loads under per-column conditions made the compiler wait for every load
+// before the first fold.
+constexpr int kGrpRegCols = 22;
+constexpr int kGrpLdsCols = 9;
+constexpr int kGrpCols = kGrpRegCols + kGrpLdsCols;
+constexpr int kGrpMax = 4;               // largest group size the workspace is laid out for
+constexpr uint32_t kGrpSpinLimit = 1u << 20;
+constexpr int kGrpAux = 2;   // cache policy of the share's loads and dl's stores: each byte is used once
+template <int T>
+constexpr int grp_lds_bytes() { return 2 * kGrpLdsCols * T * 16; }
+template <int T>
+constexpr int64_t grp_share_cap() { return (int64_t)kGrpCols * T; }   // vectors per member
+
+// Launch shape: 4 workgroups of 256 threads per row, two workgroups (80 KB of LDS each) per
+// CU, so that one's loads overlap the other's arithmetic.  Measured at C1 (4096 x 248320):
+// 1.09 ms, against 1.33 ms for 2 x 512 threads (one workgroup per CU: loads, exchange and
+// arithmetic in series) and the same 1.09 ms for 8 x 128 threads.
+constexpr int kGrpThreads = 256;
+constexpr int kGrp = 4;
+constexpr int64_t kRowCap = kGrp * grp_share_cap<kGrpThreads>() * 8;   // 253,952 entries
+static_assert(2 * (grp_lds_bytes<kGrpThreads>() + 512) <= 160 * 1024, "two group workgroups per CU");
+static_assert(kGrp <= kGrpMax, "workspace layout");
+
+struct alignas(64) GrpWords {
+  uint64_t w[8];   // 0-4 PairState, 5 label logit (tag 2 when this member holds the label), 6 accept partial
+};
 
 typedef uint32_t u32x4n_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_c;
+typedef __attribute__((address_space(3))) const u32x4n_t lds_vec;
 
 __device__ __forceinline__ void unpack8(const u32x4n_t& w, float* f) {
 #pragma unroll
@@ -446,162 +483,285 @@ __device__ __forceinline__ void unpack8(const u32x4n_t& w, float* f) {
   }
 }
 
-template <bool EMIT>
-__global__ __launch_bounds__(kRowThreads) void stream_row_kernel(
+__device__ __forceinline__ void put_word(uint64_t* p, float x, uint32_t tag) {
+  const uint64_t w = ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(x);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls until the word's tag is set; NaN (tag 1) once kGrpSpinLimit polls have gone by.
+__device__ __forceinline__ uint64_t get_word(const uint64_t* p) {
+  for (uint32_t k = 0;; ++k) {
+    const uint64_t w = __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((w >> 32) != 0) return w;
+    if (k == kGrpSpinLimit) return (1ull << 32) | 0x7fc00000ull;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+__device__ __forceinline__ float word_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Zeroes the ticket counter, the per-row finish counters and the exchange words.
+__global__ __launch_bounds__(256) void group_clear_kernel(uint4* __restrict__ p, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+template <int T, int G, bool EMIT>
+__global__ __launch_bounds__(T) void stream_group_kernel(
     const uint16_t* __restrict__ z, int64_t ldz, const uint16_t* __restrict__ u, int64_t ldu, int64_t v,
     const int64_t* __restrict__ labels, const float* __restrict__ weights, float c_ce, float c_kl, float inv_acc,
-    uint16_t* __restrict__ dl, int64_t ldd, float* __restrict__ row_stats) {
-  extern __shared__ __attribute__((aligned(16))) char row_lds[];
-  __shared__ PairState red[kRowThreads / 64];
-  __shared__ float red_a[kRowThreads / 64];
-  __shared__ float zy_sh;
+    uint16_t* __restrict__ dl, int64_t ldd, float* __restrict__ row_stats, int64_t n, uint32_t* __restrict__ ctl,
+    uint32_t* __restrict__ done, GrpWords* __restrict__ words) {
+  static_assert(G * 6 <= 64 && G <= kGrpMax, "one wave polls every peer word; workspace layout");
+  extern __shared__ __attribute__((aligned(16))) char grp_raw[];
+  __shared__ PairState red[T / 64];
+  __shared__ float red_a[T / 64];
+  __shared__ uint32_t ticket_sh;
+  __shared__ float peer[G][6];
+  __shared__ uint32_t peer_tag[G];
+  lds_c* lds = (lds_c*)grp_raw;
   const int tid = threadIdx.x;
-  const int64_t r = blockIdx.x;
-  // each row through a buffer resource of its own length (accesses past it read 0 and
-  // store nothing); vector i of this thread at byte tid * 16 + i * kRowThreads * 16
-  const uint32_t row_bytes = (uint32_t)(v * 2);
-  const __amdgpu_buffer_rsrc_t zrs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(z + r * ldz), 0, row_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t urs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(u + r * ldu), 0, row_bytes, 0x00020000);
-  const int voff = tid * 16;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid == 0) ticket_sh = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const uint32_t ticket = __builtin_amdgcn_readfirstlane(ticket_sh);   // uniform: descriptors stay scalar
+  const int64_t r = ticket / G;
+  const int h = (int)(ticket % G);
+  if (r >= n) return;   // only with a workspace that group_clear_kernel did not zero
   const int nvec = (int)(v >> 3);
-  const int full = nvec / kRowThreads, rem = nvec % kRowThreads;   // vectors i < full exist in every thread
+  const int share = (nvec + G - 1) / G;
+  const int b = h * share;
+  const int cnt = nvec - b < share ? (nvec - b > 0 ? nvec - b : 0) : share;
+  const int full = cnt / T, rem = cnt % T;   // vectors i < full exist in every thread
   auto has = [&](int i) { return i < full || (i == full && tid < rem); };
-  auto slot = [&](int i) { return reinterpret_cast<u32x4n_t*>(row_lds + (i * kRowThreads + tid) * 16); };
+  // the share through buffer resources of its own length (accesses past it read 0, store nothing)
+  const uint32_t share_bytes = (uint32_t)cnt * 16;
+  const __amdgpu_buffer_rsrc_t zrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(z + r * ldz + (int64_t)b * 8), 0, share_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(u + r * ldu + (int64_t)b * 8), 0, share_bytes, 0x00020000);
+  const int voff = tid * 16;
+  // LDS slots of column i >= kGrpRegCols
+  auto zcol = [](int i) { return i - kGrpRegCols; };
+  auto ucol = [](int i) { return kGrpLdsCols + i - kGrpRegCols; };
+  auto zslot = [&](int i) { return (lds_vec*)(lds + (zcol(i) * T + tid) * 16); };
+  auto uslot = [&](int i) { return (lds_vec*)(lds + (ucol(i) * T + tid) * 16); };
+  auto zblock = [&](int i) { return lds + (zcol(i) * T + wave * 64) * 16; };   // the wave's 1 KB of a column
+  auto ublock = [&](int i) { return lds + (ucol(i) * T + wave * 64) * 16; };
+  // phase 1: issue every load of the share, then (max, sum-exp) of z and u and
+  // A = sum exp(u - m_u)(u - z) in issue order
+  u32x4n_t zr[kGrpRegCols], ur[kGrpRegCols];
+  // column offsets in the lane's own offset (the part the buffer range check is certain to
+  // cover), the scalar offset 0
+  uint32_t vo = voff;
+#pragma unroll
+  for (int i = 0; i < kGrpRegCols; ++i) {
+    zr[i] = __builtin_amdgcn_raw_buffer_load_b128(zrs, vo, 0, kGrpAux);
+    ur[i] = __builtin_amdgcn_raw_buffer_load_b128(urs, vo, 0, kGrpAux);
+    vo += T * 16;   // formed here, not hoisted into one register per column
+    asm volatile("" : "+v"(vo));
+  }
+#pragma unroll
+  for (int i = kGrpRegCols; i < kGrpCols; ++i) {   // lane l of a wave fills the slot of thread 64 wave + l
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(zrs, (__attribute__((address_space(3))) void*)zblock(i), 16, vo, 0, 0,
+                                             kGrpAux);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(urs, (__attribute__((address_space(3))) void*)ublock(i), 16, vo, 0, 0,
+                                             kGrpAux);
+    vo += T * 16;
+    asm volatile("" : "+v"(vo));
+  }
+  // The label's entries are read on their own, after the share's loads (at a clamped index,
+  // so without a branch that would wait for them): picking them out of the columns, or
+  // patching dl[y] inside the emit loop, costs selects on every vector.
   const int64_t y = labels[r];
-  // phase 1: (max, sum-exp) of z and u and A = sum exp(u - m_u)(u - z); z kept on chip
-  u32x4n_t zreg[kRowRegVec];
+  const bool mine = y >= 8 * (int64_t)b && y < 8 * (int64_t)(b + cnt);   // this share holds the label
+  const int lab_tid = mine ? (int)((y >> 3) - b) % T : -1;
+  const int64_t yc = y < 0 ? 0 : (y < v ? y : v - 1);
+  const float zy_at = bf16_to_f32(z[r * ldz + yc]), uy_at = bf16_to_f32(u[r * ldu + yc]);
+  const float zy = mine ? zy_at : 0.f, uy = mine ? uy_at : 0.f;
   PairState st = pair_init();
-  int soff = 0;
+  auto fold = [&](int i, const u32x4n_t& zv, const u32x4n_t& uv) {
+    float zf[8], uf[8];
+    unpack8(zv, zf);
+    unpack8(uv, uf);
+    pair_update<8>(st, zf, uf);
+  };
 #pragma unroll
-  for (int g = 0; g < kRowVec; g += kRowGroup) {
-    u32x4n_t zv[kRowGroup], uv[kRowGroup];
+  for (int i = 0; i < kGrpRegCols; ++i)
+    if (has(i)) fold(i, zr[i], ur[i]);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's LDS fills have landed
 #pragma unroll
-    for (int k = 0; k < kRowGroup; ++k) {
-      const int i = g + k;
-      if (i < kRowVec && has(i)) {
-        zv[k] = __builtin_amdgcn_raw_buffer_load_b128(zrs, voff, soff, 2);
-        uv[k] = __builtin_amdgcn_raw_buffer_load_b128(urs, voff, soff, 0);
-      }
-      soff += kRowThreads * 16;   // formed here, not hoisted into one SGPR per vector
-      asm volatile("" : "+s"(soff));
+  for (int i = kGrpRegCols; i < kGrpCols; ++i)
+    if (has(i)) {
+      const u32x4n_t zv = *zslot(i), uv = *uslot(i);
+      fold(i, zv, uv);
     }
+  st = wave_reduce(st);
+  if ((tid & 63) == 0) red[wave] = st;
+  __syncthreads();
+
+  // exchange: publish this member's partials, collect the others'
+  GrpWords* mw = words + r * G;
+  if (tid == 0) {
+    PairState p = red[0];
 #pragma unroll
-    for (int k = 0; k < kRowGroup; ++k) {
-      const int i = g + k;
-      if (i < kRowVec && has(i)) {
-        float zf[8], uf[8];
-        unpack8(zv[k], zf);
-        unpack8(uv[k], uf);
-        pair_update<8>(st, zf, uf);
-        const int q = i * kRowThreads + tid;
-        if ((y >> 3) == q) {   // this vector holds the label entry (y in [0, V)): one writer,
-                               // read after the barriers below; zy_sh is not read otherwise
-          float x = zf[0];
+    for (int w = 1; w < T / 64; ++w) p = pair_merge(p, red[w]);
+    const float part[6] = {p.mz, p.sz, p.mu, p.su, p.A, zy};
 #pragma unroll
-          for (int e = 1; e < 8; ++e) x = (int)(y & 7) == e ? zf[e] : x;
-          zy_sh = x;
-        }
-        if (i < kRowLdsVec)
-          *slot(i) = zv[k];
-        else
-          zreg[i < kRowLdsVec ? 0 : i - kRowLdsVec] = zv[k];
-      }
+    for (int k = 0; k < 6; ++k) {
+      put_word(&mw[h].w[k], part[k], k == 5 && mine ? 2u : 1u);
+      peer[h][k] = part[k];
+    }
+    peer_tag[h] = mine ? 2u : 1u;
+  }
+  if (wave == 0) {
+    const int lane = tid & 63;
+    const int m = lane / 6, k = lane % 6;
+    if (m < G && m != h) {
+      const uint64_t wd = get_word(&mw[m].w[k]);
+      peer[m][k] = word_value(wd);
+      if (k == 5) peer_tag[m] = (uint32_t)(wd >> 32);
     }
   }
-  st = wave_reduce(st);
-  if ((tid & 63) == 0) red[tid >> 6] = st;
   __syncthreads();
-  st = red[0];
+  st = {peer[0][0], peer[0][1], peer[0][2], peer[0][3], peer[0][4]};
 #pragma unroll
-  for (int w = 1; w < kRowThreads / 64; ++w) st = pair_merge(st, red[w]);
+  for (int m = 1; m < G; ++m) st = pair_merge(st, PairState{peer[m][0], peer[m][1], peer[m][2], peer[m][3], peer[m][4]});
+  float zy_row = 0.f;
+#pragma unroll
+  for (int m = 0; m < G; ++m)
+    if (peer_tag[m] == 2u) zy_row = peer[m][5];
   const float lz = st.mz + logf(st.sz);
   const float lu = st.mu + logf(st.su);
-  // phase 2: p, t, sum min(p, t) and dl, z from chip, u read again
+
+  // phase 2: p, t, sum min(p, t) and dl, from chip.  The register columns pass through an
+  // empty asm so that phase 1's unpacked (fp32) copies are not kept for reuse here: the
+  // packed form is half the registers.
+#pragma unroll
+  for (int i = 0; i < kGrpRegCols; ++i) asm volatile("" : "+v"(zr[i]), "+v"(ur[i]));
   const float lzl = lz * kLog2e, lul = lu * kLog2e;
   const float w = weights[r] * inv_acc;
   const float cp = y == kIgnoreIndex ? w * c_kl : w * (c_ce + c_kl), ct = w * c_kl, cy = w * c_ce;
-  const __amdgpu_buffer_rsrc_t drs =
-      __builtin_amdgcn_make_buffer_rsrc(EMIT ? dl + r * ldd : nullptr, 0, EMIT ? row_bytes : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+      EMIT ? dl + r * ldd + (int64_t)b * 8 : nullptr, 0, EMIT ? share_bytes : 0, 0x00020000);
   float acc = 0.f;
-  soff = 0;
   int sout = 0;
+  auto emit = [&](int i, const u32x4n_t& zv, const u32x4n_t& uv) {
+    float zf[8], uf[8], d[8];
+    unpack8(zv, zf);
+    unpack8(uv, uf);
 #pragma unroll
-  for (int g = 0; g < kRowVec; g += kRowGroup) {
-    u32x4n_t uv[kRowGroup];
-#pragma unroll
-    for (int k = 0; k < kRowGroup; ++k) {
-      const int i = g + k;
-      if (i < kRowVec && has(i)) uv[k] = __builtin_amdgcn_raw_buffer_load_b128(urs, voff, soff, 2);
-      soff += kRowThreads * 16;
-      asm volatile("" : "+s"(soff));
+    for (int e = 0; e < 8; ++e) {
+      const float pp = fast_exp2(__builtin_fmaf(zf[e], kLog2e, -lzl));
+      const float tt = fast_exp2(__builtin_fmaf(uf[e], kLog2e, -lul));
+      acc += min_nonneg(pp, tt);
+      d[e] = __builtin_fmaf(cp, pp, -ct * tt);
     }
+    if (EMIT) {
+      const u32x4n_t o = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]), pack_bf16x2(d[4], d[5]),
+                          pack_bf16x2(d[6], d[7])};
+      __builtin_amdgcn_raw_buffer_store_b128(o, drs, voff, sout, kGrpAux);
+    }
+  };
 #pragma unroll
-    for (int k = 0; k < kRowGroup; ++k) {
-      const int i = g + k;
-      if (i < kRowVec && has(i)) {
-        const u32x4n_t zv = i < kRowLdsVec ? *slot(i) : zreg[i < kRowLdsVec ? 0 : i - kRowLdsVec];
-        float zf[8], uf[8], d[8];
-        unpack8(zv, zf);
-        unpack8(uv[k], uf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pp = fast_exp2(__builtin_fmaf(zf[e], kLog2e, -lzl));
-          const float tt = fast_exp2(__builtin_fmaf(uf[e], kLog2e, -lul));
-          acc += min_nonneg(pp, tt);
-          d[e] = __builtin_fmaf(cp, pp, -ct * tt);
-        }
-        if (EMIT) {
-          const int64_t i0 = 8 * (int64_t)(i * kRowThreads + tid);
-          if ((uint64_t)(y - i0) < 8ull) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if (i0 + e == y) d[e] -= cy;
-          }
-          const u32x4n_t o = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]), pack_bf16x2(d[4], d[5]),
-                              pack_bf16x2(d[6], d[7])};
-          __builtin_amdgcn_raw_buffer_store_b128(o, drs, voff, sout, 2);
-        }
+  for (int i = 0; i < kGrpCols; ++i) {
+    if (has(i)) {
+      if (i < kGrpRegCols)
+        emit(i, zr[i < kGrpRegCols ? i : 0], ur[i < kGrpRegCols ? i : 0]);
+      else
+      {
+        const u32x4n_t zv = *zslot(i), uv = *uslot(i);
+        emit(i, zv, uv);
       }
-      sout += kRowThreads * 16;
-      asm volatile("" : "+s"(sout));
     }
+    sout += T * 16;
+    asm volatile("" : "+s"(sout));
+  }
+  if (EMIT && tid == lab_tid) {   // dl[y] again, with - c_ce w, once the vector holding it is stored
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    const float pp = fast_exp2(__builtin_fmaf(zy, kLog2e, -lzl));
+    const float tt = fast_exp2(__builtin_fmaf(uy, kLog2e, -lul));
+    float d = __builtin_fmaf(cp, pp, -ct * tt);
+    d -= cy;
+    dl[r * ldd + y] = (uint16_t)(pack_bf16x2(d, 0.f) & 0xffffu);
   }
   acc = wave_sum(acc);
-  if ((tid & 63) == 0) red_a[tid >> 6] = acc;
+  if ((tid & 63) == 0) red_a[wave] = acc;
   __syncthreads();
   if (tid == 0) {
     float a = red_a[0];
 #pragma unroll
-    for (int w2 = 1; w2 < kRowThreads / 64; ++w2) a += red_a[w2];
-    // CE and KL as merge_kernel forms them (labels outside [0, V) other than the ignore
-    // index make CE NaN)
-    const float yv = (y >= 0 && y < v) ? zy_sh : __builtin_nanf("");
-    float* o = row_stats + r * kRowStatWidth;
-    o[kLseZ] = lz;
-    o[kLseU] = lu;
-    o[kCE] = y == kIgnoreIndex ? lz - lz : lz - yv;
-    o[kKL] = st.A / st.su - lu + lz;
-    o[kAccept] = accept_rate_of(a, lz, lu);
-    o[kZy] = yv;
-    o[6] = 0.f;
-    o[7] = 0.f;
+    for (int w2 = 1; w2 < T / 64; ++w2) a += red_a[w2];
+    put_word(&mw[h].w[6], a, 1u);
+    const uint32_t fin = __hip_atomic_fetch_add(done + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (fin == G - 1) {   // the row's last member: accept sum in member order, then the row's statistics
+      float at = 0.f;
+#pragma unroll
+      for (int m = 0; m < G; ++m) at += m == h ? a : word_value(get_word(&mw[m].w[6]));
+      // CE and KL as merge_kernel forms them (labels outside [0, V) other than the ignore
+      // index make CE NaN)
+      const float yv = (y >= 0 && y < v) ? zy_row : __builtin_nanf("");
+      float* o = row_stats + r * kRowStatWidth;
+      o[kLseZ] = lz;
+      o[kLseU] = lu;
+      o[kCE] = y == kIgnoreIndex ? lz - lz : lz - yv;
+      o[kKL] = st.A / st.su - lu + lz;
+      o[kAccept] = accept_rate_of(at, lz, lu);
+      o[kZy] = yv;
+      o[6] = 0.f;
+      o[7] = 0.f;
+    }
   }
 }
 
+// Workspace of the group kernel: ticket counter, per-row finish counters, exchange words.
+struct GroupWs {
+  uint32_t* ctl;
+  uint32_t* done;
+  GrpWords* words;
+  size_t bytes;
+};
+
+static size_t group_ws_layout(int64_t n, void* base, GroupWs* out) {
+  const size_t b1 = 256;
+  const size_t b2 = align_up((size_t)n * sizeof(uint32_t), 256);
+  const size_t b3 = align_up((size_t)n * kGrpMax * sizeof(GrpWords), 256);
+  if (out) {
+    char* p = static_cast<char*>(base);
+    out->ctl = reinterpret_cast<uint32_t*>(p);
+    out->done = reinterpret_cast<uint32_t*>(p + b1);
+    out->words = reinterpret_cast<GrpWords*>(p + b1 + b2);
+    out->bytes = b1 + b2 + (size_t)n * kGrp * sizeof(GrpWords);
+  }
+  return b1 + b2 + b3;
+}
+
 template <bool EMIT>
-static hipError_t launch_row(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v, const SlotArgs& a,
-                             void* dl, int64_t ldd, float* row_stats, hipStream_t st) {
+static hipError_t launch_group(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v, const SlotArgs& a,
+                               void* dl, int64_t ldd, float* row_stats, const GroupWs& g, hipStream_t st) {
   static std::atomic<uint64_t> attr_done{0};
-  if (const hipError_t e =
-          ensure_dynamic_lds(reinterpret_cast<const void*>(&stream_row_kernel<EMIT>), kRowLds, attr_done))
+  constexpr int kLds = grp_lds_bytes<kGrpThreads>();
+  if (const hipError_t e = ensure_dynamic_lds(
+          reinterpret_cast<const void*>(&stream_group_kernel<kGrpThreads, kGrp, EMIT>), kLds, attr_done))
     return e;
-  NS_TIMED(EMIT ? "stream_row" : "stream_row_accept", st);
-  hipLaunchKernelGGL(stream_row_kernel<EMIT>, dim3((unsigned)a.n), dim3(kRowThreads), kRowLds, st,
-                     static_cast<const uint16_t*>(z), ldz, static_cast<const uint16_t*>(u), ldu, v, a.labels,
-                     a.weights, a.c_ce, a.c_kl, a.inv_acc, static_cast<uint16_t*>(dl), ldd, row_stats);
+  const int64_t n16 = (int64_t)(g.bytes / 16);
+  {
+    NS_TIMED("group_clear", st);
+    hipLaunchKernelGGL(group_clear_kernel, dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)), dim3(256), 0,
+                       st, reinterpret_cast<uint4*>(g.ctl), n16);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  }
+  NS_TIMED(EMIT ? "stream_group" : "stream_group_accept", st);
+  hipLaunchKernelGGL((stream_group_kernel<kGrpThreads, kGrp, EMIT>), dim3((unsigned)(a.n * kGrp)), dim3(kGrpThreads), kLds, st, static_cast<const uint16_t*>(z),
+                     ldz, static_cast<const uint16_t*>(u), ldu, v, a.labels, a.weights, a.c_ce, a.c_kl, a.inv_acc,
+                     static_cast<uint16_t*>(dl), ldd, row_stats, a.n, g.ctl, g.done, g.words);
   return hipGetLastError();
+}
+
+// The split passes and the group kernel use the workspace in turn, never together.
+size_t stream_workspace_bytes(int64_t n, int64_t v) {
+  const size_t a = stream_ws_layout(n, v, nullptr, nullptr), b = group_ws_layout(n, nullptr, nullptr);
+  return a > b ? a : b;
 }
 
 // ---------------------------------------------------------------- host dispatch
@@ -655,12 +815,14 @@ template <typename TZ, typename TU>
 static hipError_t forward_typed(const void* z, int64_t ldz, const void* u, int64_t ldu, int64_t v,
                                 const SlotArgs& a, void* dl, int64_t ldd, float* row_stats, float* metrics,
                                 void* ws, hipStream_t st) {
-  // bf16 rows that fit on chip, 16-byte aligned: one workgroup per row
+  // bf16 rows that fit on chip, 16-byte aligned: a group of workgroups per row
   if (std::is_same<TZ, uint16_t>::value && std::is_same<TU, uint16_t>::value && v % 8 == 0 && v <= kRowCap &&
       aligned16(z) && aligned16(u) && ldz % 8 == 0 && ldu % 8 == 0 &&
       (dl == nullptr || (aligned16(dl) && ldd % 8 == 0))) {
-    hipError_t e = dl != nullptr ? launch_row<true>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, st)
-                                 : launch_row<false>(z, ldz, u, ldu, v, a, nullptr, 0, row_stats, st);
+    GroupWs g;
+    group_ws_layout(a.n, ws, &g);
+    hipError_t e = dl != nullptr ? launch_group<true>(z, ldz, u, ldu, v, a, dl, ldd, row_stats, g, st)
+                                 : launch_group<false>(z, ldz, u, ldu, v, a, nullptr, 0, row_stats, g, st);
     if (e != hipSuccess) return e;
     return launch_finalize(nullptr, 1, a, row_stats, metrics, st);   // accept rates already in row_stats
   }

@@ -121,10 +121,10 @@ def test_parity_small(gpu_lib, n, v, dtype):
         np.testing.assert_allclose(_np(dl).reshape(n, v), dl_ref, rtol=1e-4, atol=1e-8)
 
 
-@pytest.mark.parametrize("n,v", [(64, 8192), (24, 40000), (16, 248_320)])
+@pytest.mark.parametrize("n,v", [(32, 8), (32, 24), (32, 1000), (64, 8192), (24, 40000), (16, 248_320), (8, 253_952)])
 def test_row_resident_path_matches_the_two_pass_path(gpu_lib, n, v):
-    """bf16 rows within the on-chip capacity run one workgroup per row (z kept on chip);
-    the same values with an fp32 teacher run the two split passes.  Both restate
+    """bf16 rows within the on-chip capacity run four workgroups per row, each keeping its
+    quarter of z and u on chip; the same values with an fp32 teacher run the two split passes.  Both restate
     objective.py:49-80 with the same per-entry formulas: metrics within 2e-6 relative, row
     statistics within fp32 summation-order error, dl equal except where an lse's last bit
     moves one entry's rounding."""
@@ -144,17 +144,23 @@ def test_row_resident_path_matches_the_two_pass_path(gpu_lib, n, v):
 
 @pytest.mark.parametrize("v", [8192, 40000])
 def test_label_pick_at_vector_and_row_edges(gpu_lib, v):
-    """Labels at the first and last entry of a row, at the edges of a 16-byte vector and in the
-    last, partly filled round of vectors of the row-resident kernel (V = 40000: 5000 vectors,
-    9 full rounds of 512 threads and 392 vectors in the tenth): z_label, CE and dl[y] exact
-    against the oracle's pick."""
+    """Labels at the first and last entry of a row, at the edges of a 16-byte vector, on both
+    sides of the boundaries between the four workgroups that share a row, at a column edge
+    and in the last, partly filled column of the last member (V = 40000: 5000 vectors, 1250 per
+    member, 4 full columns of 256 threads and 226 vectors in the fifth): z_label, CE and dl[y]
+    exact against the oracle's pick."""
     n = 16
     z, u, slots = synthetic.logits_inputs(n, v, 400 + v, DEV)
-    # vector q = 512 i + t holds entries 8q .. 8q + 7; the last full round ends at vector
-    # 512 * (nvec // 512) - 1
-    last_full = 8 * 512 * ((v // 8) // 512)
-    picks = [0, v - 1, 7, 8, v - 8, v - 9, last_full - 1, last_full - 8, last_full % v, (last_full + 8) % v,
-             8 * 511 + 7, 8 * 512, 1, 2, 3, 4]
+    # member h holds vectors h * share .. (h + 1) * share - 1; its vector h * share + 256 i + t
+    # (entries 8 q .. 8 q + 7) is column i of thread t
+    threads, members = 256, 4
+    nvec = v // 8
+    share = -(-nvec // members)
+    starts = [8 * share * h for h in range(1, members)]
+    last_cols = (nvec - (members - 1) * share) // threads * threads
+    last_partial = 8 * ((members - 1) * share + last_cols) % v
+    picks = [0, v - 1, 7, 8, 1, 2] + [e for s in starts for e in (s - 1, s)] + \
+        [8 * threads - 1, 8 * threads, last_partial, last_partial + 9]
     y = torch.tensor(picks, dtype=torch.int64, device=DEV).view(-1, 8)
     slots = synthetic.Slots(slots.weights, y, slots.valid)
     o = Objective(block_size=8)
