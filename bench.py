@@ -25,6 +25,8 @@ import time
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA, TFLOP/s
+WARMUP_MIN_S = 0.25            # untimed warmup: at least --warmup steps and at least this long
+WARMUP_MAX_STEPS = 2000
 
 METRIC = "draft slots/sec fwd+bwd CE+KL+accept @V=248k,d=5120; %MFMA & %HBM roof"
 
@@ -818,8 +820,16 @@ def measure(wl, args, config_name):
     from nanospec_amd import _lib
 
     step = wl["step"]
-    for _ in range(args.warmup):
+    # warmup: at least W steps and at least WARMUP_MIN_S of device time, so that the clocks
+    # have left their idle state (C1, about 1 ms a step and arithmetic-bound, ran 1.156 ms a
+    # kernel after 3 warmup steps and 1.063 ms after 300)
+    warm = 0
+    t_w = time.perf_counter()
+    while warm < args.warmup or (time.perf_counter() - t_w < WARMUP_MIN_S and warm < WARMUP_MAX_STEPS):
         step()
+        warm += 1
+        if warm >= args.warmup:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     # timed window: exactly K steps between two device synchronisations.  Kernel
     # durations come from HIP events the library records around each of its launches,
@@ -890,7 +900,7 @@ def measure(wl, args, config_name):
         if wl.get("per_slot_fp8_flops"):
             ideal_s += wl["per_slot_fp8_flops"] * n / (FP8_PEAK_TFLOPS * 1e12)
         step_roof["mfma_frac"] = ideal_s / (ms_per_step / 1e3)
-    out = {"value": value, "unit": "slots/s", "steps": args.steps, "warmup": args.warmup,
+    out = {"value": value, "unit": "slots/s", "steps": args.steps, "warmup": args.warmup, "warmup_steps_run": warm,
            "ms_per_step": ms_per_step, "dtype": wl["dtype"], "config": wl["config"], "roofline": roof,
            "step_roofline": step_roof, "kernels": kernels, "wall_s": wall}
     # every kernel the north star sets a target for: the HBM stream kernels and the GEMMs
@@ -969,6 +979,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": res["warmup_steps_run"],
+        "warmup_min_s": WARMUP_MIN_S,
         "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
