@@ -99,7 +99,8 @@ def test_golden_vectors(gpu_lib):
     (64, 8192, torch.float32),
     (32, 1001, torch.bfloat16),      # odd V: unaligned rows -> scalar path
     (16, 40000, torch.bfloat16),     # several vocab splits with a ragged last split
-    (8, 250_008, torch.bfloat16),    # a bf16 row past the on-chip capacity (249,856): two passes
+    (8, 250_008, torch.bfloat16),    # a bf16 row within the on-chip capacity (253,952): group path
+    (8, 253_960, torch.bfloat16),    # a bf16 row past the on-chip capacity: two passes
 ])
 def test_parity_small(gpu_lib, n, v, dtype):
     z, u, slots = synthetic.logits_inputs(n, v, 7 + n + v, DEV)
