@@ -276,18 +276,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Wait until at most N of this wave's global loads and stores are outstanding and every
-// LDS operation is done, then a workgroup barrier (vmcnt N in bits 3:0 and 15:14,
-// expcnt 7, lgkmcnt 0).
-template <int N>
-__device__ __forceinline__ void vm_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt field");
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // acc += A[a0:a0+256, :K] . B[b0:b0+256, :K]^T, both row-major with K contiguous and
 // K a multiple of BK.
 //

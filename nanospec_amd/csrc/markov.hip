@@ -17,10 +17,12 @@ namespace {
 
 constexpr int TM = 256;          // w2.grad rows (vocab) per workgroup tile
 constexpr int TN = 256;          // w2.grad columns (rank) per workgroup tile
-constexpr int TK = 64;           // tokens per LDS stage
+constexpr int TK = 32;           // tokens per LDS stage
 constexpr int kThreads = 256;    // 4 waves as 2 (vocab) x 2 (rank), 128 x 128 each
-constexpr int kStage = TK * TN * 2;   // 32 KB per operand per stage (64 K rows x 512 B)
-constexpr int kLds = 4 * kStage;      // 2 stages x 2 operands
+constexpr int kStage = TK * TN * 2;   // 16 KB per operand per stage (32 K rows x 512 B)
+constexpr int kRing = 4;              // stages in LDS: fills run three stages ahead
+constexpr int kUnroll = 8;            // stages per loop iteration (a multiple of kRing)
+constexpr int kFills = TK * 512 / 1024 / 4;   // 16-byte-per-lane fills per wave per operand per stage
 
 // E[t] = w1[prev[t]] (bf16 rows of r entries); ids outside [0, V) read row 0 (the forward
 // has already turned that row's loss NaN).
@@ -39,6 +41,26 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const int64_t* __restr
 // (rank columns), both K-contiguous through transposed LDS reads.
 struct KnFrags {
   TrFrag a[4], b[4];
+};
+
+// A TK-row operand stage (512-byte rows, the rows' 16-byte chunks XOR-swizzled by 4 (row & 3))
+// fetched straight into LDS: fill i of wave wv writes rows 2 (wv kFills + i) and the next.
+struct DmaStageKN {
+  uint32_t off[kFills];
+  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kFills; ++i) {
+      const int row = 2 * (wv * kFills + i) + (lane >> 5);
+      const int cn = (lane & 31) ^ (4 * (row & 3));
+      int64_t col = c0 + cn * 8;
+      col = col < cmax ? col : c0;
+      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    dma16(base, off[i], dst + (wv * kFills + i) * 1024);
+  }
 };
 
 __device__ __forceinline__ void read_kn_frags(KnFrags& f, const lds_t* sa, const lds_t* sb, int kk,
@@ -60,16 +82,16 @@ __device__ __forceinline__ void mma_kn(f32x16_t (&acc)[4][4], const KnFrags& f) 
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(f.a[i]), tr_join(f.b[j]), acc[i][j], 0, 0, 0);
 }
 
-// All four steps of one stage, fragments double-buffered across steps; mem(kk) issues
-// step kk's share of the next stage's fills.
+// All TK / 16 steps of one stage, fragments double-buffered across steps; mem(kk) issues
+// step kk's share of a later stage's fills.
 template <typename Mem>
 __device__ __forceinline__ void stage_kn(f32x16_t (&acc)[4][4], const lds_t* sa, const lds_t* sb,
                                          const uint32_t (&ta)[4], const uint32_t (&tbv)[4], Mem&& mem) {
   KnFrags f[2];
   read_kn_frags(f[0], sa, sb, 0, ta, tbv);
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    if (kk < 3) read_kn_frags(f[(kk + 1) & 1], sa, sb, kk + 1, ta, tbv);
+  for (int kk = 0; kk < TK / 16; ++kk) {
+    if (kk + 1 < TK / 16) read_kn_frags(f[(kk + 1) & 1], sa, sb, kk + 1, ta, tbv);
     __builtin_amdgcn_sched_barrier(0);
     mem(kk);
     __builtin_amdgcn_sched_barrier(0);
@@ -108,13 +130,22 @@ struct Dw2Params {
 // filled row-major ([t][v], [t][c]) into LDS and read K-contiguous with tr_b16.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void dw2_kernel(Dw2Params p) {
-  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
-  lds_t* lds = (lds_t*)lds_raw;
+  // one LDS array per ring buffer: the compiler tells fills of one buffer from reads of
+  // another only across distinct objects (with offsets into one array it waited for every
+  // outstanding fill before each stage's fragment reads)
+  __shared__ __attribute__((aligned(16))) char ring0[2 * kStage];
+  __shared__ __attribute__((aligned(16))) char ring1[2 * kStage];
+  __shared__ __attribute__((aligned(16))) char ring2[2 * kStage];
+  __shared__ __attribute__((aligned(16))) char ring3[2 * kStage];
+  static_assert(kRing == 4, "one array per ring buffer");
+  auto ring = [&](int b) -> lds_t* {
+    return b == 0 ? (lds_t*)ring0 : b == 1 ? (lds_t*)ring1 : b == 2 ? (lds_t*)ring2 : (lds_t*)ring3;
+  };
   const int vt = blockIdx.x / p.ct, ctile = blockIdx.x % p.ct;
   const int64_t v0 = (int64_t)vt * TM, c0 = (int64_t)ctile * TN;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wv >> 1, wn = wv & 1;
-  DmaTileKN ta, tb;
+  DmaStageKN ta, tb;
   ta.init(p.ldd, v0, p.v, wv);
   tb.init(p.r, c0, p.r, wv);
   uint32_t tra[4], trb[4];
@@ -126,7 +157,6 @@ void dw2_kernel(Dw2Params p) {
   const char* pa = reinterpret_cast<const char*>(p.dl + v0);
   const char* pb = reinterpret_cast<const char*>(p.e + c0);
   const int64_t sa_bytes = (int64_t)TK * p.ldd * 2, sb_bytes = (int64_t)TK * p.r * 2;
-  auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * 2 * kStage; };
   const int KTf = (int)(p.n / TK);
   f32x16_t acc[4][4];
 #pragma unroll
@@ -135,36 +165,53 @@ void dw2_kernel(Dw2Params p) {
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-  if (KTf > 0) {
+  // stage t lives in buffer t % kRing.  The loop below is unrolled by kUnroll so that every
+  // buffer is a compile-time choice; only the first stage of an iteration still waits for all
+  // outstanding fills (the compiler's count does not survive the loop's back edge).
+  auto fill = [&](int t, int b, int i) {
+    lds_t* dst = ring(b);
+    ta.issue(pa + t * sa_bytes, dst, wv, i);
+    tb.issue(pb + t * sb_bytes, dst + kStage, wv, i);
+  };
+  // stages 0 .. kRing - 2 go out first; stage t + kRing - 1 goes out during stage t, into
+  // the buffer of stage t - 1, which every wave has finished reading at stage t's barrier
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ta.issue(pa, buf(0), wv, i);
-      tb.issue(pb, buf(0) + kStage, wv, i);
-    }
-  }
-  for (int t = 0; t < KTf; ++t) {
-    fill_barrier();   // stage t landed; everyone is done with stage t - 1's buffer
-    // the next stage's 16 fills per wave, four before each step's MFMAs: all 16 at once
-    // stalled the waves behind their own burst of L2 misses (10% slower)
-    const bool more = t + 1 < KTf;
-    stage_kn(acc, buf(t), buf(t) + kStage, tra, trb, [&](int kk) {
-      if (more) {
+  for (int t = 0; t < kRing - 1; ++t)
+    if (t < KTf)
 #pragma unroll
-        for (int i = 2 * kk; i < 2 * kk + 2; ++i) {
-          ta.issue(pa + (t + 1) * sa_bytes, buf(t + 1), wv, i);
-          tb.issue(pb + (t + 1) * sb_bytes, buf(t + 1) + kStage, wv, i);
-        }
+      for (int i = 0; i < kFills; ++i) fill(t, t, i);
+  for (int t0 = 0; t0 < KTf; t0 += kUnroll) {
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) {
+      const int t = t0 + j;
+      if (t < KTf) {
+        // stage t landed: this wave's later fills (stages t + 1, t + 2, 2 kFills each) may still fly
+        if (t + 2 < KTf)
+          vm_barrier<4 * kFills>();
+        else if (t + 1 < KTf)
+          vm_barrier<2 * kFills>();
+        else
+          vm_barrier<0>();
+        const int tn = t + kRing - 1;
+        const lds_t* cur = ring(j % kRing);
+        stage_kn(acc, cur, cur + kStage, tra, trb, [&](int kk) {
+          if (tn < KTf) {
+#pragma unroll
+            for (int i = kk * kFills / (TK / 16); i < (kk + 1) * kFills / (TK / 16); ++i)
+              fill(tn, (j + kRing - 1) % kRing, i);
+          }
+        });
       }
-    });
+    }
   }
   const int kvalid = (int)(p.n - (int64_t)KTf * TK);
   if (kvalid > 0) {
     fill_barrier();
     const int64_t k0 = (int64_t)KTf * TK;
-    load_kn_tail(lds, p.dl + k0 * p.ldd, p.ldd, v0, p.v, kvalid);
-    load_kn_tail(lds + kStage, p.e + k0 * p.r, p.r, c0, p.r, kvalid);
+    load_kn_tail(ring(0), p.dl + k0 * p.ldd, p.ldd, v0, p.v, kvalid);
+    load_kn_tail(ring(0) + kStage, p.e + k0 * p.r, p.r, c0, p.r, kvalid);
     __syncthreads();
-    stage_kn(acc, lds, lds + kStage, tra, trb, [](int) {});
+    stage_kn(acc, ring(0), ring(0) + kStage, tra, trb, [](int) {});
   }
   const int lane = threadIdx.x & 63, h = lane >> 5;
 #pragma unroll
@@ -371,11 +418,9 @@ hipError_t markov_backward(const void* dl, int64_t ldd, const void* weight, int6
     p.w2g = static_cast<uint16_t*>(w2_grad); p.ldg2 = ldg2;
     p.n = n; p.v = v; p.r = r;
     p.ct = (int)((r + TN - 1) / TN);
-    static std::atomic<uint64_t> attr_done{0};
-    if ((e = ensure_dynamic_lds(reinterpret_cast<const void*>(&dw2_kernel), kLds, attr_done)) != hipSuccess) return e;
     NS_TIMED("markov_dw2", st);
     const int grid = (int)((v + TM - 1) / TM) * p.ct;
-    hipLaunchKernelGGL(dw2_kernel, dim3(grid), dim3(kThreads), kLds, st, p);
+    hipLaunchKernelGGL(dw2_kernel, dim3(grid), dim3(kThreads), 0, st, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {

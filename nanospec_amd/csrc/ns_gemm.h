@@ -145,6 +145,18 @@ __device__ __forceinline__ void fill_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Wait until at most N of this wave's global loads and stores are outstanding and every
+// LDS operation is done, then a workgroup barrier (vmcnt N in bits 3:0 and 15:14,
+// expcnt 7, lgkmcnt 0).
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Workgroup -> (tile t, split s) map for a grid of TT x S workgroups, one per CU at a
 // time.  Workgroups are dispatched round-robin over the 8 XCDs, and the workgroups of
 // one XCD share its L2.  With xa > 0 the grid runs in rounds of xa * xb workgroups per

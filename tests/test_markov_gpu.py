@@ -138,11 +138,12 @@ def _assert_grads(dl, mk, g1, w1_grad, w2_grad, keep=None):
 
 
 @pytest.mark.parametrize("n,v,d,r,id_range", [
-    (72, 8200, 128, 64, None),        # ragged vocab tile, a 64-token stage plus an 8-token tail
+    (72, 8200, 128, 64, None),        # ragged vocab tile, two 32-token stages plus an 8-token tail
     (256, 4096, 256, 256, None),      # the reference rank, whole stages only
     (1000, 2048, 192, 128, 16),       # long runs of repeated ids (index_add_ segments of ~60)
-    (1536, 16384, 256, 256, None),    # 24 token stages, 64 vocab tiles
-    (40, 4096, 128, 64, None),        # fewer tokens than one stage: the register path alone
+    (1536, 16384, 256, 256, None),    # 48 token stages (six unrolled groups of 8), 64 vocab tiles
+    (24, 4096, 128, 64, None),        # fewer tokens than one stage: the register path alone
+    (1000, 4096, 128, 64, None),      # 31 stages (a partial unrolled group) plus an 8-token tail
     (128, 2048, 128, 512, 8),         # rank 512: two rank tiles in the w2.grad GEMM
 ])
 def test_markov_backward_matches_oracle(gpu_lib, n, v, d, r, id_range):
