@@ -52,156 +52,6 @@ static_assert(kAccReadNops == 3, "the epilogue's s_nop sequence below is written
 
 
 
-// Per-lane byte offsets of a 256 (rows) x 64 (K) bf16 tile of a K-contiguous matrix,
-// relative to the uniform address of element (r0, k0).  Thread t loads rows
-// i*32 + t/8 (i = 0..7), 16-byte chunk t%8; rows >= rmax are clamped (never used).
-struct RowTile {
-  uint32_t off[8];
-  __device__ __forceinline__ void init(int64_t ld, int64_t r0, int64_t rmax) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int64_t row = r0 + i * 32 + (tid >> 3);
-      row = row < rmax ? row : rmax - 1;
-      off[i] = (uint32_t)(((row - r0) * ld + (tid & 7) * 8) * 2);
-    }
-  }
-  __device__ __forceinline__ void load(uint4 (&v)[8], const char* base) const {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint4*>(base + off[i]);
-  }
-  __device__ __forceinline__ void load_one(uint4& v, const char* base, int i) const {
-    v = *reinterpret_cast<const uint4*>(base + off[i]);
-  }
-  // One row group of a stage with only `kvalid` valid K entries: chunks past the end
-  // read chunk 0 instead (in bounds) and are zeroed when stored (store_row with kvalid).
-  __device__ __forceinline__ void load_one_clamped(uint4& v, const char* base, int i, int kvalid) const {
-    const int c = (threadIdx.x & 7) * 8;
-    v = *reinterpret_cast<const uint4*>(base + off[i] - (c < kvalid ? 0u : (uint32_t)(c * 2)));
-  }
-  // Stage with only `kvalid` (< BK) valid K entries: the rest reads chunk 0 and is zeroed.
-  __device__ __forceinline__ void load_tail(uint4 (&v)[8], const char* base, int kvalid) const {
-    const int c = (threadIdx.x & 7) * 8;
-    const bool ok = c < kvalid;
-    const uint32_t back = ok ? 0u : (uint32_t)(c * 2);
-    const uint32_t keep = ok ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint4 x = *reinterpret_cast<const uint4*>(base + off[i] - back);
-      x.x &= keep; x.y &= keep; x.z &= keep; x.w &= keep;
-      v[i] = x;
-    }
-  }
-};
-
-__device__ __forceinline__ void store_row(const uint4& v, lds_t* lds, int i, int kvalid = BK) {
-  const int tid = threadIdx.x;
-  const int row = i * 32 + (tid >> 3);
-  const uint32_t keep = (tid & 7) * 8 < kvalid ? 0xffffffffu : 0u;
-  const u32x4_t y = {v.x & keep, v.y & keep, v.z & keep, v.w & keep};
-  *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(lds + lds_off(row, tid & 7)) = y;
-}
-
-__device__ __forceinline__ void store_tile(const uint4 (&v)[8], lds_t* lds) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = i * 32 + (tid >> 3);
-    const u32x4_t y = {v[i].x, v[i].y, v[i].z, v[i].w};
-    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(lds + lds_off(row, tid & 7)) = y;
-  }
-}
-
-// Per-lane offsets of a 64 (K rows) x 256 (columns) bf16 tile of a row-major [K, cols]
-// matrix that is transposed into the [col][K] swizzled LDS layout.  Thread t handles the
-// (4-row, 8-column) groups t and t + 256; columns >= cmax are clamped (never used).
-struct ColTile {
-  uint32_t off[2];
-  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int grp = threadIdx.x + h * kThreads;
-      const int rg = grp >> 5, cg = grp & 31;
-      int64_t col = c0 + cg * 8;
-      col = col < cmax ? col : cmax - 8;
-      off[h] = (uint32_t)(((int64_t)rg * 4 * ld + (col - c0)) * 2);
-    }
-  }
-  __device__ __forceinline__ void load(uint4 (&v)[2][4], const char* base, int64_t ld_bytes) const {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[h][j] = *reinterpret_cast<const uint4*>(base + off[h] + j * ld_bytes);
-  }
-  // K row j of group h with only `kvalid` valid K rows: rows past the end read the
-  // stage's first row instead (in bounds) and are zeroed when stored (store_col_t).
-  __device__ __forceinline__ void load_one_clamped(uint4& v, const char* base, int64_t ld_bytes, int h, int j,
-                                                   int kvalid) const {
-    const int rg = (threadIdx.x + h * kThreads) >> 5;
-    v = *reinterpret_cast<const uint4*>(base + (rg * 4 + j < kvalid ? off[h] + j * ld_bytes : 0));
-  }
-  __device__ __forceinline__ void load_tail(uint4 (&v)[2][4], const char* base, int64_t ld_bytes, int kvalid) const {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int rg = (threadIdx.x + h * kThreads) >> 5;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool ok = rg * 4 + j < kvalid;
-        const uint32_t keep = ok ? 0xffffffffu : 0u;
-        uint4 x = *reinterpret_cast<const uint4*>(base + (ok ? off[h] + j * ld_bytes : 0));
-        x.x &= keep; x.y &= keep; x.z &= keep; x.w &= keep;
-        v[h][j] = x;
-      }
-    }
-  }
-};
-
-// Column c of group h of a transposed tile (see store_tile_t): one 8-byte LDS store.
-__device__ __forceinline__ void store_col_t(const uint4 (&v)[2][4], lds_t* lds, int h, int c, int kvalid) {
-  const int grp = threadIdx.x + h * kThreads;
-  const int rg = grp >> 5, cg = grp & 31;
-  // K rows 4 rg + j >= kvalid hold clamped re-reads: zero them
-  const uint32_t m01 = (rg * 4 + 0 < kvalid ? 0xffffu : 0u) | (rg * 4 + 1 < kvalid ? 0xffff0000u : 0u);
-  const uint32_t m23 = (rg * 4 + 2 < kvalid ? 0xffffu : 0u) | (rg * 4 + 3 < kvalid ? 0xffff0000u : 0u);
-  const uint32_t w0[4] = {v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w};
-  const uint32_t w1[4] = {v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w};
-  const uint32_t w2[4] = {v[h][2].x, v[h][2].y, v[h][2].z, v[h][2].w};
-  const uint32_t w3[4] = {v[h][3].x, v[h][3].y, v[h][3].z, v[h][3].w};
-  const int sh = (c & 1) * 16;
-  const uint32_t e0 = (w0[c >> 1] >> sh) & 0xffffu;
-  const uint32_t e1 = (w1[c >> 1] >> sh) & 0xffffu;
-  const uint32_t e2 = (w2[c >> 1] >> sh) & 0xffffu;
-  const uint32_t e3 = (w3[c >> 1] >> sh) & 0xffffu;
-  const int row = cg * 8 + c;
-  const int off = lds_off(row, rg >> 1) + (rg & 1) * 8;
-  const u32x2_t y = {(e0 | (e1 << 16)) & m01, (e2 | (e3 << 16)) & m23};
-  *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + off) = y;
-}
-
-__device__ __forceinline__ void store_tile_t(const uint4 (&v)[2][4], lds_t* lds) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int grp = threadIdx.x + h * kThreads;
-    const int rg = grp >> 5, cg = grp & 31;
-    const uint32_t w[4][4] = {{v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w},
-                              {v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w},
-                              {v[h][2].x, v[h][2].y, v[h][2].z, v[h][2].w},
-                              {v[h][3].x, v[h][3].y, v[h][3].z, v[h][3].w}};
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int sh = (c & 1) * 16;
-      const uint32_t e0 = (w[0][c >> 1] >> sh) & 0xffffu;
-      const uint32_t e1 = (w[1][c >> 1] >> sh) & 0xffffu;
-      const uint32_t e2 = (w[2][c >> 1] >> sh) & 0xffffu;
-      const uint32_t e3 = (w[3][c >> 1] >> sh) & 0xffffu;
-      const int row = cg * 8 + c;
-      const int off = lds_off(row, rg >> 1) + (rg & 1) * 8;
-      const u32x2_t y = {e0 | (e1 << 16), e2 | (e3 << 16)};
-      *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + off) = y;
-    }
-  }
-}
-
 // MFMA operand fragments of one 16-wide K step for this wave's 128 x 128 block.
 struct Frags {
   bf16x8_t a[4], b[4];
@@ -234,37 +84,6 @@ __device__ __forceinline__ void load_frag_pair(Frags& f, const lds_t* la, const 
 __device__ __forceinline__ constexpr int quarter_begin(int q, int n) {
   return q == 0 ? 0 : q == 1 ? n / 8 : q == 2 ? n / 4 : q == 3 ? (n * 5) / 8 : n;
 }
-
-// One BK stage: 64 MFMAs in 16 groups of 4.  With one wave per SIMD the matrix core is
-// busy only while its wave issues MFMAs, and a burst of 16-byte global loads or LDS
-// stores stalls in-order issue; so after each MFMA group the wave issues a few of the
-// stage's other instructions: the next step's fragment reads (groups 0-1) and
-// mem(kk, q) -- the next stage's LDS stores (steps 0-1) and the prefetch of the stage
-// after it (steps 2-3).  sched_barrier keeps the compiler from regrouping them.
-template <typename Mem>
-__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const lds_t* la, const lds_t* lb, Mem&& mem) {
-  Frags f[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) load_frag_pair(f[0], la, lb, 0, i);
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    const int cb = kk & 1;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[cb].a[q], f[cb].b[j], acc[q][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (kk < 3 && q < 2) {
-        load_frag_pair(f[cb ^ 1], la, lb, kk + 1, 2 * q);
-        load_frag_pair(f[cb ^ 1], la, lb, kk + 1, 2 * q + 1);
-      }
-      mem(kk, q);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-}
-
 
 // Wait for this wave's LDS operations only, then a workgroup barrier (outstanding global
 // loads, LDS fills included, keep flying).  s_waitcnt encoding: vmcnt 63, expcnt 7,
@@ -420,42 +239,100 @@ __device__ __forceinline__ bool gemm_nt(f32x16_t (&acc)[4][4], const uint16_t* _
                        reinterpret_cast<const char*>(B + b0 * ldb), (int)(K / BK), lds, tail);
 }
 
-// acc += A[a0:a0+256, k0:k0+64 KT] . B[k0:k0+64 KT, c0:c0+256] over KT full stages,
-// A row-major (K contiguous), B row-major [K, cols].  Both operands go global -> LDS
-// without registers, as in gemm_nt; B fragments use transposed LDS reads.  Per stage t:
-//   steps 0-2: the next step's 12 fragment reads (4 A, 8 B halves), one per MFMA;
-//   step 0: the B fills of stage t + 1 in the even MFMA slots;
-//   step 3: fill_barrier first (as in gemm_nt_tiles), then in its first eight slots stage
-//           t + 1's step-0 fragments, and the A fills of stage t + 2 in the odd slots.
-// Every other slot rather than eight in a row keeps a CU's line misses in flight below
-// what its L1 queues (2% off the dh GEMM at C2).  Spreading further, over three steps as
-// gemm_nt_tiles does, measured 7% slower here; so did fills after the fragment reads
-// (slots 8-15).  Ends with a barrier.  KT >= 1.
-__device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
-                                            int64_t a0, int64_t amax, const uint16_t* __restrict__ B,
-                                            int64_t ldb, int64_t c0, int64_t cmax, int64_t k0, int KT,
-                                            lds_t* lds) {
+// ---- dh GEMM: 32-K stages in a 4-deep LDS ring ----------------------------------------------
+// acc += A[a0:a0+256, k0:k0+32 S] . B[k0:k0+32 S, c0:c0+256] (+ a partial stage of kv < 32
+// K entries), A row-major (K contiguous), B row-major [K, cols].  Both operands go straight into
+// LDS; the fills of stage t + 3 go out during stage t, so every fill has two to three stages of
+// lead (with 64-K stages in two buffers the last fills of a stage had about half a stage).  The
+// fills are issued through inline asm (dma16_asm): with the builtin the compiler, unable to tell
+// a stage's fragment reads from a later stage's fills, waited for every outstanding fill before
+// each read (9.37 ms against 7.57 ms at C2); the explicit vmcnt waits below order them.  The
+// four ring buffers are separate LDS arrays and the stage loop is unrolled by 8, so every
+// fragment address is a constant offset: with a computed buffer index the loop ran 2% slower.
+//
+// A stage: 256 rows x 64 B (32 bf16 along K); chunk c of row m at m * 64 + ((c ^ sw4(m)) << 4),
+// sw4(m) = (m >> 2) & 3, so the 16 rows of a ds_read_b128 lane group hit 16 distinct 16-byte
+// bank slots.  B stage: 32 rows x 512 B, as DmaTileKNR<32> (transposed fragment reads).
+constexpr int BK2 = 32;                     // K per ring stage
+constexpr int kRingStage = BM * BK2 * 2;    // 16 KB per operand per stage
+constexpr int kRingBuf = 2 * kRingStage;    // one ring buffer: A then B
+constexpr int kRingUnroll = 8;              // stages per loop iteration (a multiple of 4)
+
+__device__ __forceinline__ int a32_off(int m, int c) { return m * 64 + ((c ^ ((m >> 2) & 3)) << 4); }
+
+// A stage fetched straight into LDS: fill i of wave wv writes rows 16 (4 wv + i) .. +15; lane l
+// fetches logical chunk (l & 3) ^ sw4(row) of row 16 (4 wv + i) + l / 4.  Rows at or past rmax
+// re-read row rmax - 1 (their results are discarded).
+struct DmaTileA32 {
+  uint32_t off[4];
+  __device__ __forceinline__ void init(int64_t ld_bytes, int64_t r0, int64_t rmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (wv * 4 + i) * 16 + (lane >> 2);
+      int64_t r = r0 + row;
+      r = r < rmax ? r : rmax - 1;
+      const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+      off[i] = (uint32_t)((r - r0) * ld_bytes + chunk * 16);
+    }
+  }
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    dma16_asm(base, off[i], dst + (wv * 4 + i) * 1024);
+  }
+};
+
+// A partial stage (kv < BK2 valid K entries, a multiple of 8) through registers into one ring
+// buffer: K entries at or past kv are zero; A rows at or past amax and B columns at or past cmax
+// re-read row a0 / column c0 (their results are discarded).
+__device__ __forceinline__ void load_ring_tail(lds_t* dst, const uint16_t* A, int64_t lda, int64_t a0, int64_t amax,
+                                               const uint16_t* B, int64_t ldb, int64_t c0, int64_t cmax, int kv) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {   // A: 256 rows x 4 chunks
+    const int ci = i * 256 + tid;
+    const int m = ci >> 2, c = ci & 3;
+    int64_t row = a0 + m;
+    row = row < amax ? row : a0;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (c * 8 < kv) x = *reinterpret_cast<const uint4*>(A + row * lda + c * 8);
+    const u32x4_t y = {x.x, x.y, x.z, x.w};
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(dst + a32_off(m, c)) = y;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {   // B: 32 K rows x 32 chunks of 8 columns
+    const int ci = i * 256 + tid;
+    const int k = ci >> 5, cn = ci & 31;
+    int64_t col = c0 + cn * 8;
+    col = col < cmax ? col : c0;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (k < kv) x = *reinterpret_cast<const uint4*>(B + (int64_t)k * ldb + col);
+    const u32x4_t y = {x.x, x.y, x.z, x.w};
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(dst + kRingStage + k * 512 +
+                                                                  ((cn ^ (4 * (k & 3))) << 4)) = y;
+  }
+}
+
+// S full stages from k0, then (kv > 0) one partial stage.  `ring(b)` is ring buffer b (b < 4).
+// Per stage t (two 16-K MFMA steps, one fragment read per MFMA slot in slots 0-11):
+//   step 0: stage t's step-1 fragments; fills 0-3 of stage t + 3 in slots 1, 5, 9, 13;
+//   step 1: first a barrier (stage t + 1 landed, and every wave is past stage t - 1's reads),
+//           then stage t + 1's step-0 fragments and fills 4-7 of stage t + 3 in slots 1, 5, 9,
+//           13, into stage t - 1's buffer.
+// Fills and reads past the last stage re-read the last stage into a buffer nobody reads, so the
+// loop body has no conditions but its stage count (branches in it made the compiler shuttle
+// the accumulators between register files).  Ends with a barrier.
+template <typename Ring>
+__device__ __forceinline__ void gemm_nn_ring(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
+                                             int64_t a0, int64_t amax, const uint16_t* __restrict__ B,
+                                             int64_t ldb, int64_t c0, int64_t cmax, int64_t k0, int S, int kv,
+                                             const Ring& ring) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  DmaTile<256> ta;
-  DmaTileKN tb;
-  ta.init(lda * 2, a0, amax, wv);
-  tb.init(ldb, c0, cmax, wv);
-  const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
-  const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
-  const int64_t ldb_stage = (int64_t)BK * ldb * 2;
-  auto clampt = [&](int t) -> int64_t { return (int64_t)(t < KT - 1 ? t : KT - 1); };
-  auto buf = [&](int t) -> lds_t* { return lds + (t & 1) * 2 * kStageBytes; };
   const int lane = threadIdx.x & 63;
   const int wm = wv >> 1, wn = wv & 1;
   const int r = lane & 31, kh = lane >> 5;
   uint32_t tb_addr[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) tb_addr[i] = tr_base(wn, i);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ta.issue(pa, buf(0), wv, i);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) tb.issue(pb, buf(0) + kStageBytes, wv, i);
-  fill_barrier();
   bf16x8_t fa[2][4];
   TrFrag fb[2][4];
   // read op o (0..11) of step kk from stage buffer `sb` into set `c`: A i, B i lo, B i hi
@@ -463,120 +340,82 @@ __device__ __forceinline__ void gemm_nn_dma(f32x16_t (&acc)[4][4], const uint16_
     const int i = o / 3, part = o % 3;
     if (part == 0)
       fa[c][i] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-          sb + lds_off(wm * 128 + i * 32 + r, kk * 2 + kh));
+          sb + a32_off(wm * 128 + i * 32 + r, kk * 2 + kh));
     else if (part == 1)
-      fb[c][i].lo = tr_read(sb + kStageBytes, tb_addr[i] + kk * 8192);
+      fb[c][i].lo = tr_read(sb + kRingStage, tb_addr[i] + kk * 8192);
     else
-      fb[c][i].hi = tr_read(sb + kStageBytes, tb_addr[i] + kk * 8192 + 2048);
+      fb[c][i].hi = tr_read(sb + kRingStage, tb_addr[i] + kk * 8192 + 2048);
   };
+  auto mma = [&](int c, int q, int j) {
+    acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][q], tr_join(fb[c][j]), acc[q][j], 0, 0, 0);
+  };
+  if (S > 0) {
+    DmaTileA32 ta;
+    DmaTileKNR<BK2> tb;
+    ta.init(lda * 2, a0, amax, wv);
+    tb.init(ldb, c0, cmax, wv);
+    const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
+    const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
+    const int64_t sb_bytes = (int64_t)BK2 * ldb * 2;
+    auto fill = [&](int t, lds_t* dst, int f) {   // fill f (0-7) of stage min(t, S - 1): A 0-3, B 4-7
+      const int64_t tc = t < S - 1 ? t : S - 1;
+      if (f < 4)
+        ta.issue(pa + tc * BK2 * 2, dst, wv, f);
+      else
+        tb.issue_asm(pb + tc * sb_bytes, dst + kRingStage, wv, f - 4);
+    };
 #pragma unroll
-  for (int o = 0; o < 12; ++o) read_op(0, buf(0), 0, o);
-  {
-    const int64_t t1 = clampt(1);
+    for (int t = 0; t < 3; ++t)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ta.issue(pa + t1 * BK * 2, buf(1), wv, i);
-  }
-  for (int t = 0; t < KT; ++t) {
-    const lds_t* cur = buf(t);
-    lds_t* nxt = buf(t + 1);
-    const int64_t t1 = clampt(t + 1), t2 = clampt(t + 2);
+      for (int f = 0; f < 8; ++f) fill(t, ring(t), f);
+    vm_barrier<16>();   // stage 0 landed; stages 1 and 2 may still fly
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int cb = kk & 1;
-      if (kk == 3) fill_barrier();
+    for (int o = 0; o < 12; ++o) read_op(0, ring(0), 0, o);
+    for (int t0 = 0; t0 < S; t0 += kRingUnroll) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int j = 0; j < kRingUnroll; ++j) {
+        const int t = t0 + j;
+        if (t < S) {
+          const lds_t* cur = ring(j % 4);
+          const lds_t* nxt = ring((j + 1) % 4);
+          lds_t* far = ring((j + 3) % 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int sl = q * 4 + j;
-          acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][q], tr_join(fb[cb][j]), acc[q][j], 0, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          if (kk < 3 && sl < 12) read_op(cb ^ 1, cur, kk + 1, sl);
-          if (kk == 0 && !(sl & 1)) tb.issue(pb + t1 * ldb_stage, nxt + kStageBytes, wv, sl >> 1);
-          if (kk == 3 && sl < 8) {
-            const int u = sl;
-            if (u < 4) {
-              read_op(0, nxt, 0, 2 * u);
-              read_op(0, nxt, 0, 2 * u + 1);
-            } else {
-              read_op(0, nxt, 0, 4 + u);
+          for (int kk = 0; kk < 2; ++kk) {
+            // stage t + 1 landed: stage t + 2's 8 fills and stage t + 3's first 4 may fly
+            if (kk == 1) vm_barrier<12>();
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) {
+                const int sl = q * 4 + jj;
+                mma(kk, q, jj);
+                __builtin_amdgcn_sched_barrier(0);
+                if (sl < 12) read_op(kk ^ 1, kk == 0 ? cur : nxt, kk ^ 1, sl);
+                if ((sl & 3) == 1) fill(t + 3, far, kk * 4 + (sl >> 2));
+                __builtin_amdgcn_sched_barrier(0);
+              }
             }
           }
-          if (kk == 3 && (sl & 1)) ta.issue(pa + t2 * BK * 2, buf(t), wv, sl >> 1);
-          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
   }
+  if (kv > 0) {
+    fill_barrier();   // every fill landed; every wave is past its last ring read
+    const int64_t kt = k0 + (int64_t)S * BK2;
+    load_ring_tail(ring(0), A + kt, lda, a0, amax, B + kt * ldb, ldb, c0, cmax, kv);
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+      for (int o = 0; o < 12; ++o) read_op(0, ring(0), kk, o);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) mma(0, q, jj);
+    }
+  }
   fill_barrier();
-}
-
-// acc += A[a0:a0+256, k0:k1] . B[k0:k1, c0:c0+256] with A row-major (K contiguous) and
-// B row-major [K, cols] (columns contiguous, transposed through LDS).  Entries with
-// K >= kmax are zero.  Ends with a barrier.  Same stage structure as gemm_nt.
-__device__ __forceinline__ void gemm_nn(f32x16_t (&acc)[4][4], const uint16_t* __restrict__ A, int64_t lda,
-                                        int64_t a0, int64_t amax, const uint16_t* __restrict__ B, int64_t ldb,
-                                        int64_t c0, int64_t cmax, int64_t k0, int64_t k1, int64_t kmax,
-                                        lds_t* lds) {
-  const int KT = (int)((k1 - k0 + BK - 1) / BK);
-  if (KT <= 0) return;
-  RowTile ta;
-  ColTile tb;
-  ta.init(lda, a0, amax);
-  tb.init(ldb, c0, cmax);
-  const int64_t ldb_bytes = ldb * 2;
-  const char* pa = reinterpret_cast<const char*>(A + a0 * lda + k0);
-  const char* pb = reinterpret_cast<const char*>(B + k0 * ldb + c0);
-  uint4 ra[8], rb[2][4];
-  // stage bases and valid K count; stages past the end re-read the last one
-  auto stage_of = [&](int kt, const char*& a, const char*& b, int& kv) {
-    kt = kt < KT - 1 ? kt : KT - 1;
-    const int64_t kvalid = kmax - (k0 + (int64_t)kt * BK);
-    kv = kvalid < BK ? (int)kvalid : BK;
-    a = pa + (int64_t)kt * BK * 2;
-    b = pb + (int64_t)kt * BK * ldb_bytes;
-  };
-  int kv1;
-  {
-    const char *a, *b;
-    int kv;
-    stage_of(0, a, b, kv);
-    ta.load_tail(ra, a, kv);
-    tb.load_tail(rb, b, ldb_bytes, kv);
-    store_tile(ra, lds);
-    store_tile_t(rb, lds + kStageBytes);
-    __syncthreads();
-    stage_of(1, a, b, kv1);
-    ta.load_tail(ra, a, kv1);
-    tb.load_tail(rb, b, ldb_bytes, kv1);
-  }
-  int ckv = kv1;  // valid K entries of the stage held in registers
-  for (int kt = 0; kt < KT; ++kt) {
-    const lds_t* cur = lds + (kt & 1) * 2 * kStageBytes;
-    lds_t* nxt = lds + ((kt + 1) & 1) * 2 * kStageBytes;
-    const char *na, *nb;
-    int nkv;
-    stage_of(kt + 2, na, nb, nkv);
-    mma_stage(acc, cur, cur + kStageBytes, [&](int kk, int q) {
-      if (kk == 1) {
-#pragma unroll
-        for (int idx = 0; idx < 16; ++idx) {
-          if (idx < quarter_begin(q, 16) || idx >= quarter_begin(q + 1, 16)) continue;
-          store_col_t(rb, nxt + kStageBytes, idx >> 3, idx & 7, ckv);
-        }
-        return;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i < quarter_begin(q, 8) || i >= quarter_begin(q + 1, 8)) continue;
-        if (kk == 0) store_row(ra[i], nxt, i, ckv);
-        if (kk == 2) ta.load_one_clamped(ra[i], na, i, nkv);
-        if (kk == 3) tb.load_one_clamped(rb[i >> 2][i & 3], nb, ldb_bytes, i >> 2, i & 3, nkv);
-      }
-    });
-    ckv = nkv;
-    __syncthreads();
-  }
 }
 
 // ------------------------------------------------------------------ head kernel
@@ -1354,8 +1193,14 @@ struct BwdParams {
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void dh_kernel(BwdParams p) {
-  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
-  lds_t* lds = (lds_t*)lds_raw;
+  // the GEMM's LDS ring: one array per buffer (see gemm_nn_ring)
+  __shared__ __attribute__((aligned(16))) char ring0[kRingBuf];
+  __shared__ __attribute__((aligned(16))) char ring1[kRingBuf];
+  __shared__ __attribute__((aligned(16))) char ring2[kRingBuf];
+  __shared__ __attribute__((aligned(16))) char ring3[kRingBuf];
+  auto ring = [&](int b) -> lds_t* {
+    return b == 0 ? (lds_t*)ring0 : b == 1 ? (lds_t*)ring1 : b == 2 ? (lds_t*)ring2 : (lds_t*)ring3;
+  };
   // Tile order.  Workgroups go round-robin to the 8 XCDs and run in rounds of
   // C = xa * xb per XCD (one per CU).  With xa > 0 each round of one XCD is a block of
   // xa token tiles x xb d tiles of one K split, so a K stage reads xa + xb distinct
@@ -1396,14 +1241,11 @@ void dh_kernel(BwdParams p) {
   const int64_t m0 = (int64_t)mt * BM, c0 = (int64_t)ct * BN;
   f32x16_t acc[4][4];
   zero_acc(acc);
-  // full stages straight into LDS; a partial last stage (V % BK != 0) through registers,
-  // where entries past V are zeroed
-  const int kfull = (int)(p.v / BK);
-  const int kt_dma_end = kt1 < kfull ? kt1 : kfull;
-  if (kt_dma_end > kt0)
-    gemm_nn_dma(acc, p.dl, p.ldd, m0, p.n, B, ldb, c0, cols, (int64_t)kt0 * BK, kt_dma_end - kt0, lds);
-  if (kt1 > kt_dma_end)
-    gemm_nn(acc, p.dl, p.ldd, m0, p.n, B, ldb, c0, cols, (int64_t)kt_dma_end * BK, (int64_t)kt1 * BK, p.v, lds);
+  // this split's K range [kt0 BK, min(kt1 BK, V)): full 32-K stages straight into LDS, a
+  // partial last one (V % 32 != 0) through registers with entries past V zeroed
+  const int64_t kb = (int64_t)kt0 * BK, ke = (int64_t)kt1 * BK < p.v ? (int64_t)kt1 * BK : p.v;
+  const int S = (int)((ke - kb) / BK2), kv = (int)(ke - kb - (int64_t)S * BK2);
+  gemm_nn_ring(acc, p.dl, p.ldd, m0, p.n, B, ldb, c0, cols, kb, S, kv, ring);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int h = lane >> 5;
@@ -1703,12 +1545,9 @@ hipError_t lmhead_backward_ext(const void* dl, int64_t ldd, const void* weight, 
   const size_t b_part2 = align_up((size_t)pl.ksplit2 * n * r * sizeof(float), 256);
   p.part2 = reinterpret_cast<float*>(static_cast<char*>(ws) + b_part);
   void* norm_ws = static_cast<char*>(ws) + b_part + b_part2;
-  static std::atomic<uint64_t> attr_done{0};
-  if (const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&dh_kernel), kGemmLds, attr_done))
-    return e;
   {
-    NS_TIMED("dh_gemm", st);
-    hipLaunchKernelGGL(dh_kernel, dim3(pl.grid), dim3(kThreads), kGemmLds, st, p);
+    NS_TIMED("dh_gemm", st);   // 128 KB of static LDS (the ring), none dynamic
+    hipLaunchKernelGGL(dh_kernel, dim3(pl.grid), dim3(kThreads), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -22,7 +22,7 @@ constexpr int kThreads = 256;    // 4 waves as 2 (vocab) x 2 (rank), 128 x 128 e
 constexpr int kStage = TK * TN * 2;   // 16 KB per operand per stage (32 K rows x 512 B)
 constexpr int kRing = 4;              // stages in LDS: fills run three stages ahead
 constexpr int kUnroll = 8;            // stages per loop iteration (a multiple of kRing)
-constexpr int kFills = TK * 512 / 1024 / 4;   // 16-byte-per-lane fills per wave per operand per stage
+constexpr int kFills = DmaTileKNR<TK>::NI;   // fills per wave per operand per stage
 
 // E[t] = w1[prev[t]] (bf16 rows of r entries); ids outside [0, V) read row 0 (the forward
 // has already turned that row's loss NaN).
@@ -41,26 +41,6 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const int64_t* __restr
 // (rank columns), both K-contiguous through transposed LDS reads.
 struct KnFrags {
   TrFrag a[4], b[4];
-};
-
-// A TK-row operand stage (512-byte rows, the rows' 16-byte chunks XOR-swizzled by 4 (row & 3))
-// fetched straight into LDS: fill i of wave wv writes rows 2 (wv kFills + i) and the next.
-struct DmaStageKN {
-  uint32_t off[kFills];
-  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < kFills; ++i) {
-      const int row = 2 * (wv * kFills + i) + (lane >> 5);
-      const int cn = (lane & 31) ^ (4 * (row & 3));
-      int64_t col = c0 + cn * 8;
-      col = col < cmax ? col : c0;
-      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
-    }
-  }
-  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
-    dma16(base, off[i], dst + (wv * kFills + i) * 1024);
-  }
 };
 
 __device__ __forceinline__ void read_kn_frags(KnFrags& f, const lds_t* sa, const lds_t* sb, int kk,
@@ -145,7 +125,7 @@ void dw2_kernel(Dw2Params p) {
   const int64_t v0 = (int64_t)vt * TM, c0 = (int64_t)ctile * TN;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wv >> 1, wn = wv & 1;
-  DmaStageKN ta, tb;
+  DmaTileKNR<TK> ta, tb;
   ta.init(p.ldd, v0, p.v, wv);
   tb.init(p.r, c0, p.r, wv);
   uint32_t tra[4], trb[4];

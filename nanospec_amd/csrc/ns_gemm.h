@@ -38,6 +38,19 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t voff, lds_t* ds
                                            voff, soff, 0, 0);
 }
 
+// dma16 issued through inline asm.  The compiler then sees no LDS write in flight, so it adds
+// no waits for one before LDS reads (with the builtin it waited for every outstanding fill
+// before a read it could not prove disjoint); the caller's own vmcnt waits must order each
+// fill before the reads of its data.  Same instruction, descriptor and LDS layout as dma16.
+__device__ __forceinline__ void dma16_asm(const char* base, uint32_t voff, lds_t* dst) {
+  typedef uint32_t u32x4s_t __attribute__((ext_vector_type(4)));
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const u32x4s_t rs = {(uint32_t)b, (uint32_t)(b >> 32) & 0xffffu, 0xffffffffu, 0x00020000u};
+  const uint32_t m0v = (uint32_t)reinterpret_cast<uintptr_t>(dst);
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "s"(m0v)
+               : "memory", "m0");
+}
+
 // A ROWS-row operand tile (128-byte rows) fetched straight into LDS (dma16).  Each of the
 // WAVES waves issues NI = ROWS / (8 WAVES) instructions per stage; instruction i of wave wv
 // fills the 1 KB LDS block wv * NI + i, i.e. rows 8 (wv * NI + i) .. +8.  Lane l writes the
@@ -102,6 +115,32 @@ struct DmaTileKN {
   }
   __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
     dma16(base, off[i], dst + (wv * 8 + i) * 1024);
+  }
+};
+
+// The same for a ROWS-row stage (ROWS = 8 * fills per wave): fill i of wave wv writes rows
+// 2 (wv NI + i) and the next.
+template <int ROWS>
+struct DmaTileKNR {
+  static constexpr int NI = ROWS / 8;
+  static_assert(NI * 8 == ROWS, "two rows per fill, four waves");
+  uint32_t off[NI];
+  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = 2 * (wv * NI + i) + (lane >> 5);
+      const int cn = (lane & 31) ^ (4 * (row & 3));
+      int64_t col = c0 + cn * 8;
+      col = col < cmax ? col : c0;
+      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
+    dma16(base, off[i], dst + (wv * NI + i) * 1024);
+  }
+  __device__ __forceinline__ void issue_asm(const char* base, lds_t* dst, int wv, int i) const {
+    dma16_asm(base, off[i], dst + (wv * NI + i) * 1024);
   }
 };
 
