@@ -457,10 +457,11 @@ constexpr int grp_lds_bytes() { return 2 * kGrpLdsCols * T * 16; }
 template <int T>
 constexpr int64_t grp_share_cap() { return (int64_t)kGrpCols * T; }   // vectors per member
 
-// Launch shape: 4 workgroups of 256 threads per row, two workgroups (80 KB of LDS each) per
-// CU, so that one's loads overlap the other's arithmetic.  Measured at C1 (4096 x 248320):
-// 1.09 ms, against 1.33 ms for 2 x 512 threads (one workgroup per CU: loads, exchange and
-// arithmetic in series) and the same 1.09 ms for 8 x 128 threads.
+// Launch shape: 4 workgroups of 256 threads per row, two workgroups (72 KB of LDS each) per
+// CU, so that one's loads overlap the other's arithmetic.  Measured at C1 (4096 x 248320), with
+// an earlier register/LDS column split: 1.09 ms, against 1.33 ms for 2 x 512 threads (one
+// workgroup per CU: loads, exchange and arithmetic in series) and the same 1.09 ms for 8 x 128
+// threads; the kernel now runs 1.06 ms.
 constexpr int kGrpThreads = 256;
 constexpr int kGrp = 4;
 constexpr int64_t kRowCap = kGrp * grp_share_cap<kGrpThreads>() * 8;   // 253,952 entries
