@@ -18,6 +18,7 @@
 // take the split passes.
 // Every reduction has a fixed order, so results are bitwise reproducible.
 #include <atomic>
+#include <cstdlib>
 #include <type_traits>
 
 #include "ns_internal.h"
@@ -468,6 +469,23 @@ constexpr int64_t kRowCap = kGrp * grp_share_cap<kGrpThreads>() * 8;   // 253,95
 static_assert(2 * (grp_lds_bytes<kGrpThreads>() + 512) <= 160 * 1024, "two group workgroups per CU");
 static_assert(kGrp <= kGrpMax, "workspace layout");
 
+// Test settings of the exchange (environment NS_DEBUG_GROUP_DROP_MEMBER, _SPIN_LIMIT): a
+// member that publishes nothing, and the poll limit.  Unset: -1 and kGrpSpinLimit.
+struct GrpDebug {
+  int drop_member;
+  uint32_t spin_limit;
+};
+
+static GrpDebug group_debug() {
+  GrpDebug d{-1, kGrpSpinLimit};
+  if (const char* e = getenv("NS_DEBUG_GROUP_DROP_MEMBER"); e && *e) d.drop_member = atoi(e);
+  if (const char* e = getenv("NS_DEBUG_GROUP_SPIN_LIMIT"); e && *e) {
+    const long x = atol(e);
+    d.spin_limit = x < 1 ? 1u : x > (long)kGrpSpinLimit ? kGrpSpinLimit : (uint32_t)x;
+  }
+  return d;
+}
+
 struct alignas(64) GrpWords {
   uint64_t w[8];   // 0-4 PairState, 5 label logit (tag 2 when this member holds the label), 6 accept partial
 };
@@ -489,12 +507,12 @@ __device__ __forceinline__ void put_word(uint64_t* p, float x, uint32_t tag) {
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls until the word's tag is set; NaN (tag 1) once kGrpSpinLimit polls have gone by.
-__device__ __forceinline__ uint64_t get_word(const uint64_t* p) {
+// Polls until the word's tag is set; NaN (tag 1) once `limit` polls have gone by.
+__device__ __forceinline__ uint64_t get_word(const uint64_t* p, uint32_t limit) {
   for (uint32_t k = 0;; ++k) {
     const uint64_t w = __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if ((w >> 32) != 0) return w;
-    if (k == kGrpSpinLimit) return (1ull << 32) | 0x7fc00000ull;
+    if (k >= limit) return (1ull << 32) | 0x7fc00000ull;
     __builtin_amdgcn_s_sleep(2);
   }
 }
@@ -512,7 +530,7 @@ __global__ __launch_bounds__(T) void stream_group_kernel(
     const uint16_t* __restrict__ z, int64_t ldz, const uint16_t* __restrict__ u, int64_t ldu, int64_t v,
     const int64_t* __restrict__ labels, const float* __restrict__ weights, float c_ce, float c_kl, float inv_acc,
     uint16_t* __restrict__ dl, int64_t ldd, float* __restrict__ row_stats, int64_t n, uint32_t* __restrict__ ctl,
-    uint32_t* __restrict__ done, GrpWords* __restrict__ words) {
+    uint32_t* __restrict__ done, GrpWords* __restrict__ words, GrpDebug dbg) {
   static_assert(G * 6 <= 64 && G <= kGrpMax, "one wave polls every peer word; workspace layout");
   extern __shared__ __attribute__((aligned(16))) char grp_raw[];
   __shared__ PairState red[T / 64];
@@ -610,7 +628,7 @@ __global__ __launch_bounds__(T) void stream_group_kernel(
     const float part[6] = {p.mz, p.sz, p.mu, p.su, p.A, zy};
 #pragma unroll
     for (int k = 0; k < 6; ++k) {
-      put_word(&mw[h].w[k], part[k], k == 5 && mine ? 2u : 1u);
+      if (h != dbg.drop_member) put_word(&mw[h].w[k], part[k], k == 5 && mine ? 2u : 1u);
       peer[h][k] = part[k];
     }
     peer_tag[h] = mine ? 2u : 1u;
@@ -619,7 +637,7 @@ __global__ __launch_bounds__(T) void stream_group_kernel(
     const int lane = tid & 63;
     const int m = lane / 6, k = lane % 6;
     if (m < G && m != h) {
-      const uint64_t wd = get_word(&mw[m].w[k]);
+      const uint64_t wd = get_word(&mw[m].w[k], dbg.spin_limit);
       peer[m][k] = word_value(wd);
       if (k == 5) peer_tag[m] = (uint32_t)(wd >> 32);
     }
@@ -693,12 +711,12 @@ __global__ __launch_bounds__(T) void stream_group_kernel(
     float a = red_a[0];
 #pragma unroll
     for (int w2 = 1; w2 < T / 64; ++w2) a += red_a[w2];
-    put_word(&mw[h].w[6], a, 1u);
+    if (h != dbg.drop_member) put_word(&mw[h].w[6], a, 1u);
     const uint32_t fin = __hip_atomic_fetch_add(done + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (fin == G - 1) {   // the row's last member: accept sum in member order, then the row's statistics
       float at = 0.f;
 #pragma unroll
-      for (int m = 0; m < G; ++m) at += m == h ? a : word_value(get_word(&mw[m].w[6]));
+      for (int m = 0; m < G; ++m) at += m == h ? a : word_value(get_word(&mw[m].w[6], dbg.spin_limit));
       // CE and KL as merge_kernel forms them (labels outside [0, V) other than the ignore
       // index make CE NaN)
       const float yv = (y >= 0 && y < v) ? zy_row : __builtin_nanf("");
@@ -755,7 +773,7 @@ static hipError_t launch_group(const void* z, int64_t ldz, const void* u, int64_
   NS_TIMED(EMIT ? "stream_group" : "stream_group_accept", st);
   hipLaunchKernelGGL((stream_group_kernel<kGrpThreads, kGrp, EMIT>), dim3((unsigned)(a.n * kGrp)), dim3(kGrpThreads), kLds, st, static_cast<const uint16_t*>(z),
                      ldz, static_cast<const uint16_t*>(u), ldu, v, a.labels, a.weights, a.c_ce, a.c_kl, a.inv_acc,
-                     static_cast<uint16_t*>(dl), ldd, row_stats, a.n, g.ctl, g.done, g.words);
+                     static_cast<uint16_t*>(dl), ldd, row_stats, a.n, g.ctl, g.done, g.words, group_debug());
   return hipGetLastError();
 }
 

@@ -96,3 +96,26 @@ def test_group_path_on_two_streams(gpu_lib):
         for out, want in zip(outs, wants):
             for g, w_ in zip(out[:3], want):
                 assert torch.equal(g, w_), rep
+
+
+def test_group_wait_runs_out_to_nan_and_the_next_call_is_exact(gpu_lib, monkeypatch):
+    """The exchange's bounded wait, forced from the host: member 1 of every row publishes nothing
+    (NS_DEBUG_GROUP_DROP_MEMBER=1) and each poll loop gives up after 64 polls
+    (NS_DEBUG_GROUP_SPIN_LIMIT=64).  The call returns; the members that waited take NaN
+    statistics, so dl holds NaN and accept_len_sum is NaN.  The next call without the settings
+    (its counters and words cleared again) equals the eager result bit for bit."""
+    lib = gpu_lib
+    n, v = 64, 40000
+    inp = _inputs(n, v, 17)
+    want = _eager(lib, inp)
+    monkeypatch.setenv("NS_DEBUG_GROUP_DROP_MEMBER", "1")
+    monkeypatch.setenv("NS_DEBUG_GROUP_SPIN_LIMIT", "64")
+    metrics, row_stats, dl = _eager(lib, inp)
+    assert torch.isnan(metrics[4]).item()            # accept_len_sum
+    assert torch.isnan(row_stats[:, 4]).all().item()  # every row's accept rate
+    assert torch.isnan(dl.float()).any().item()
+    monkeypatch.delenv("NS_DEBUG_GROUP_DROP_MEMBER")
+    monkeypatch.delenv("NS_DEBUG_GROUP_SPIN_LIMIT")
+    again = _eager(lib, inp)
+    for g, w_ in zip(again, want):
+        assert torch.equal(g, w_)
