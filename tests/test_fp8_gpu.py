@@ -67,7 +67,8 @@ def _assert_fp8_logits(got, x, codes, scale):
 @pytest.mark.parametrize("n,d,v", [
     (64, 256, 1024),
     (200, 384, 2048),
-    (3072, 128, 16384),   # 24 token tiles: 32 splits in three rounds of 8 x 4 XCD blocks
+    (3072, 128, 16384),   # 12 token tiles: 64 splits in three rounds of 4 x 8 XCD blocks
+    (300, 256, 1152),     # the last vocab tile half past V, the last token tile partial
 ])
 def test_fp8_linear_matches_oracle(gpu_lib, n, d, v):
     x, codes, scale = synthetic.fp8_teacher_inputs(n, d, v, 11 + n, DEV)
