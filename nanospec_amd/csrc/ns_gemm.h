@@ -94,32 +94,12 @@ struct DmaTile {
   }
 };
 
-// B operand [K rows, cols] (cols contiguous) fetched straight into a row-major LDS
-// stage: 64 K rows of 512 bytes, the 16-byte chunk cn of row k stored at physical
-// chunk cn ^ (4 (k & 3)), which keeps the transposed fragment reads (tr_b16) free of
-// bank conflicts.  Instruction i of wave wv fills rows 2 (wv * 8 + i) + {0, 1}; lane l
-// writes physical chunk l % 32 of row 2 (wv * 8 + i) + l / 32.  Column chunks at or
+// B operand [K rows, cols] (cols contiguous) fetched straight into a row-major LDS stage
+// of ROWS K rows of 512 bytes (ROWS = 8 x fills per wave, four waves), the 16-byte chunk cn
+// of row k stored at physical chunk cn ^ (4 (k & 3)), which keeps the transposed fragment
+// reads (tr_b16) free of bank conflicts.  Fill i of wave wv writes rows 2 (wv NI + i) + {0,
+// 1}; lane l writes physical chunk l % 32 of row 2 (wv NI + i) + l / 32.  Column chunks at or
 // past cmax re-read the tile's first chunk (discarded by the caller).
-struct DmaTileKN {
-  uint32_t off[8];
-  __device__ __forceinline__ void init(int64_t ld, int64_t c0, int64_t cmax, int wv) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 2 * (wv * 8 + i) + (lane >> 5);
-      const int cn = (lane & 31) ^ (4 * (row & 3));
-      int64_t col = c0 + cn * 8;
-      col = col < cmax ? col : c0;
-      off[i] = (uint32_t)((row * ld + (col - c0)) * 2);
-    }
-  }
-  __device__ __forceinline__ void issue(const char* base, lds_t* dst, int wv, int i) const {
-    dma16(base, off[i], dst + (wv * 8 + i) * 1024);
-  }
-};
-
-// The same for a ROWS-row stage (ROWS = 8 * fills per wave): fill i of wave wv writes rows
-// 2 (wv NI + i) and the next.
 template <int ROWS>
 struct DmaTileKNR {
   static constexpr int NI = ROWS / 8;
@@ -146,7 +126,7 @@ struct DmaTileKNR {
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
-// B fragment i (32 columns) of step kk from a DmaTileKN stage, as two transposed reads:
+// B fragment i (32 columns) of step kk from a DmaTileKNR stage, as two transposed reads:
 // ds_read_b64_tr_b16 gives lane 16 g + x of a 16-lane group element x % 4 of the
 // 8-byte pieces addressed by lanes 16 g + 4 j + x / 4, j = 0..3.  Lane 16 g + 4 j + m
 // addresses row kbase + j, columns nb + 4 m .. +3, so lane 16 g + x receives
