@@ -78,13 +78,6 @@ __device__ __forceinline__ void load_frag_pair(Frags& f, const lds_t* la, const 
       lb + lds_off(wn * 128 + i * 32 + r, kk * 2 + kh));
 }
 
-// [begin, end) of the memory operations issued after MFMA group q (of 4) when a step
-// carries n of them: 1/8, 1/8, 3/8, 3/8 of n, so the early groups leave room for the
-// next step's fragment reads.
-__device__ __forceinline__ constexpr int quarter_begin(int q, int n) {
-  return q == 0 ? 0 : q == 1 ? n / 8 : q == 2 ? n / 4 : q == 3 ? (n * 5) / 8 : n;
-}
-
 // Wait for this wave's LDS operations only, then a workgroup barrier (outstanding global
 // loads, LDS fills included, keep flying).  s_waitcnt encoding: vmcnt 63, expcnt 7,
 // lgkmcnt 0.

@@ -42,6 +42,8 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t voff, lds_t* ds
 // no waits for one before LDS reads (with the builtin it waited for every outstanding fill
 // before a read it could not prove disjoint); the caller's own vmcnt waits must order each
 // fill before the reads of its data.  Same instruction, descriptor and LDS layout as dma16.
+// M0 is reserved to the compiler, which does not honour the clobber: a kernel using this
+// must not also use dma16 or anything else that sets M0 (the dh GEMM uses only this form).
 __device__ __forceinline__ void dma16_asm(const char* base, uint32_t voff, lds_t* dst) {
   typedef uint32_t u32x4s_t __attribute__((ext_vector_type(4)));
   const uint64_t b = reinterpret_cast<uint64_t>(base);
