@@ -100,11 +100,12 @@ constexpr int kBStage = FN * kQBlock;        // 32 KB of activation codes
 constexpr int kStage = kAStage + kBStage;
 constexpr int kRing = 2;
 constexpr int kRingLds = kRing * kStage;     // 128 KB
-constexpr int kLseOff = kRingLds;            // [FN][2] fp32 running (max, sum-exp) per token
-constexpr int kFp8Lds = kLseOff + FN * 8;
 constexpr int kOutRow = FM * 2 + 16;         // bf16 output row in the LDS transpose (+16 B)
 constexpr int kOutTokens = 128;              // tokens per output pass (two passes per tile)
-static_assert(kOutTokens * kOutRow <= kRingLds, "output transpose fits in the ring");
+constexpr int kOutOff = kStage;              // the transpose: ring buffer 1 and 3.5 KB past it
+constexpr int kLseOff = kOutOff + kOutTokens * kOutRow;   // [FN][2] fp32 running (max, sum-exp)
+constexpr int kFp8Lds = kLseOff + FN * 8;
+static_assert(kOutOff + kOutTokens * kOutRow <= kLseOff && kLseOff % 16 == 0, "LDS layout");
 static_assert(kFp8Lds <= 160 * 1024, "fp8 head LDS");
 
 // s_waitcnt vmcnt(0) lgkmcnt(0) (expcnt not waited): gfx9 encoding, vmcnt[3:0] in bits
@@ -173,6 +174,29 @@ __device__ __forceinline__ void wait_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The lane's index in its wave, formed where it is used (mbcnt over an opaque zero) rather
+// than kept from the thread-id register, which the stage loop would otherwise spill.
+__device__ __forceinline__ int lane_here() {
+  uint32_t z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, z));
+}
+
+// DmaTile::init with the lane formed in place (same offsets): the next tile's weight rows
+// are set up inside the stage loop.
+template <int ROWS, int WAVES>
+__device__ __forceinline__ void tile_init_here(DmaTile<ROWS, WAVES>& tt, int64_t ld_bytes, int64_t r0, int64_t rmax, int wv) {
+  const int lane = lane_here();
+#pragma unroll
+  for (int i = 0; i < DmaTile<ROWS, WAVES>::NI; ++i) {
+    const int row = (wv * DmaTile<ROWS, WAVES>::NI + i) * 8 + (lane >> 3);
+    int64_t rr = r0 + row;
+    rr = rr < rmax ? rr : rmax - 1;
+    const int chunk = (lane & 7) ^ swz(row);
+    tt.off[i] = (uint32_t)((rr - r0) * ld_bytes + chunk * 16);
+  }
+}
+
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fp8_head_kernel(Fp8Params p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
@@ -213,14 +237,30 @@ void fp8_head_kernel(Fp8Params p) {
     lse_st[2 * tid + 1] = 0.f;
   }
 
+  auto a_src = [&](int vt) -> const char* { return reinterpret_cast<const char*>(p.wq + (int64_t)vt * FM * p.ldw); };
+  auto ws_row = [&](int vt) -> const float* {   // this wave's weight-scale row block of tile vt
+    int vb = vt * (FM / kQBlock) + wm;
+    vb = vb < nvb ? vb : nvb - 1;                // a tile half past V: rows discarded
+    return p.ws + (int64_t)vb * KB;
+  };
+  DmaTile<FM, kWaves> ta;
+  bool staged = false;   // this tile's first stage in buffer 0, its fragments in registers
+  float c_cur[2], c_prev[2], xn[2], wnx;
+  i32x8_t a[2];            // [kk]: block row q's A fragments, reloaded after their last use
+  i32x8_t b[2][2];         // [j][kk]
+  f32x16_t part[2];        // [j]: the pair of MFMAs of one 32 x 32 block over 128 K
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int64_t v0 = (int64_t)vt * FM;
-    DmaTile<FM, kWaves> ta;
-    ta.init(p.ldw, v0, p.v, wv);
-    const char* pa = reinterpret_cast<const char*>(p.wq + v0 * p.ldw);
-    int vb = (int)(v0 / kQBlock) + wm;   // this wave's weight-scale row block
-    vb = vb < nvb ? vb : nvb - 1;        // a tile half past V: rows discarded
-    const float* wsrow = p.ws + (int64_t)vb * KB;
+    const char* pa = a_src(vt);
+    const float* wsrow = ws_row(vt);
+    // With an even number of stages the tile's last one sits in buffer 1, and the next tile's
+    // first stage fills buffer 0 during this tile's last two stages (its weight codes in
+    // slots 12-15 of stage KB - 2, its activation codes in slots 0-3 of stage KB - 1) while the
+    // epilogue transposes through buffer 1; otherwise each tile starts with its own fills.
+    // Waiting at each tile's start for its first fills took 11.8K cycles of a 143K-cycle tile.
+    const bool pf = vt + 1 < vt_end && (KB & 1) == 0;
+    const char* pan = a_src(vt + 1);
+    const float* wsn = ws_row(vt + 1);
 
     f32x16_t acc[4][2];
 #pragma unroll
@@ -233,35 +273,38 @@ void fp8_head_kernel(Fp8Params p) {
     // prologue: stage 0's scales, then the fills of stage 0 and stage 1's A fills (its B
     // fills go out in stage 0); wait for stage 0 only (vector-memory operations complete
     // in order)
-    float c_cur[2], c_prev[2] = {0.f, 0.f}, xn[2], wnx;
-    {
-      const float w0 = wsrow[0];
-      c_cur[0] = p.xs[xsoff[0]] * w0;
-      c_cur[1] = p.xs[xsoff[1]] * w0;
-    }
-    const int64_t k1 = KB > 1 ? kQBlock : 0;
-#pragma unroll
-    for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa, buf(0), wv, i);
-#pragma unroll
-    for (int i = 0; i < DmaTile<FN, kWaves>::NI; ++i) tb.issue(pb, buf(0) + kAStage, wv, i);
-#pragma unroll
-    for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa + k1, buf(1), wv, i);
-    static_assert(DmaTile<FM, kWaves>::NI == 4 && DmaTile<FN, kWaves>::NI == 4, "fill slots");
-    wait_barrier<kWaitPrologue>();
-
-    i32x8_t a[2];            // [kk]: block row q's A fragments, reloaded after their last use
-    i32x8_t b[2][2];         // [j][kk]
-    f32x16_t part[2];        // [j]: the pair of MFMAs of one 32 x 32 block over 128 K
+    c_prev[0] = c_prev[1] = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) part[j][e] = 0.f;
+    auto read_frags = [&]() {
+      const int fl = lane_here(), fr = fl & 31, fkh = fl >> 5;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) b[j][kk] = rd32(buf(0) + kAStage, wn * 64 + j * 32 + r, kk * 4 + kh * 2);
+        for (int kk = 0; kk < 2; ++kk) b[j][kk] = rd32(buf(0) + kAStage, wn * 64 + j * 32 + fr, kk * 4 + fkh * 2);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) a[kk] = rd32(buf(0), wm * 128 + r, kk * 4 + kh * 2);
+      for (int kk = 0; kk < 2; ++kk) a[kk] = rd32(buf(0), wm * 128 + fr, kk * 4 + fkh * 2);
+    };
+    if (!staged) {
+      tile_init_here(ta, p.ldw, v0, p.v, wv);
+      {
+        const float w0 = wsrow[0];
+        c_cur[0] = p.xs[xsoff[0]] * w0;
+        c_cur[1] = p.xs[xsoff[1]] * w0;
+      }
+      const int64_t k1 = KB > 1 ? kQBlock : 0;
+#pragma unroll
+      for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa, buf(0), wv, i);
+#pragma unroll
+      for (int i = 0; i < DmaTile<FN, kWaves>::NI; ++i) tb.issue(pb, buf(0) + kAStage, wv, i);
+#pragma unroll
+      for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pa + k1, buf(1), wv, i);
+      static_assert(DmaTile<FM, kWaves>::NI == 4 && DmaTile<FN, kWaves>::NI == 4, "fill slots");
+      wait_barrier<kWaitPrologue>();
+      read_frags();
+    }
 
     for (int t = 0; t < KB; ++t) {
       const lds_t* cb = buf(t);
@@ -269,7 +312,10 @@ void fp8_head_kernel(Fp8Params p) {
       lds_t* db = buf(t);              // stage t + 2 lands where stage t was
       const int64_t k2 = (int64_t)(t + 2) * kQBlock;
       const bool more = t + 1 < KB, fill2 = t + 2 < KB;
-      const int kn = more ? t + 1 : t;
+      const int kn = more ? t + 1 : 0;              // the next stage: this tile's or the next tile's first
+      const float* wsk = more ? wsrow : wsn;
+      const bool fill_next = pf && t == KB - 2;     // slots 12-15 fill the next tile's first stage
+      if (fill_next) tile_init_here(ta, p.ldw, v0 + FM, p.v, wv);
       // 16 MFMA slots s = 4 q + 2 j + kk; the pair (q, j) accumulates over the stage's two
       // 64-K halves into part[j], which is folded into the accumulator with the block
       // scale in slot (q + 1, j, 0), before the next pair overwrites it (sched_barrier
@@ -297,7 +343,7 @@ void fp8_head_kernel(Fp8Params p) {
               const float* xsb = p.xs + (int64_t)kn * p.n;
               xn[0] = xsb[xsoff[0]];
               xn[1] = xsb[xsoff[1]];
-              wnx = wsrow[kn];
+              wnx = wsk[kn];
             }
             // stage t + 1's B fills (activation codes), one per slot in slots 0-3 (the last
             // stage re-reads itself into the idle buffer).  That half of buffer t + 1 was last
@@ -318,6 +364,7 @@ void fp8_head_kernel(Fp8Params p) {
               const int u = s - 12;   // 0..3
               // stage t + 2's A fills (weight codes) into stage t's buffer, one per slot
               if (fill2) ta.issue(pa + k2, db, wv, u);
+              else if (fill_next) ta.issue(pan, db, wv, u);
               // stage t + 1's fragments, each right after its last use in this stage: B (j, kk)
               // in its own slot, A row 0 in the slots of block (3, 1)
               if (more) {
@@ -339,10 +386,13 @@ void fp8_head_kernel(Fp8Params p) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[3][j][e] = __builtin_fmaf(c_prev[j], part[j][e], acc[3][j][e]);
-    wait_barrier<kWaitAll>();   // no fill in flight, every wave done with the ring
+    // no fill in flight (the next tile's first stage, when prefetched, has landed), every
+    // wave done with the ring
+    wait_barrier<kWaitAll>();
 
     // bf16 tile transposed through LDS in two passes of 128 tokens, then whole 16-byte
     // chunks of output rows
+    const int etid = wv * 64 + lane_here(), er = etid & 31, ekh = (etid >> 5) & 1;   // == tid
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       if ((wn >> 1) == half) {
@@ -352,18 +402,18 @@ void fp8_head_kernel(Fp8Params p) {
           for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const int tl = (wn & 1) * 64 + j * 32 + r;
-              const int vl = wm * 128 + q * 32 + 8 * g + 4 * kh;
+              const int tl = (wn & 1) * 64 + j * 32 + er;
+              const int vl = wm * 128 + q * 32 + 8 * g + 4 * ekh;
               const u32x2_t y = {pack_bf16x2(acc[q][j][4 * g], acc[q][j][4 * g + 1]),
                                  pack_bf16x2(acc[q][j][4 * g + 2], acc[q][j][4 * g + 3])};
-              *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + tl * kOutRow + vl * 2) = y;
+              *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(lds + kOutOff + tl * kOutRow + vl * 2) = y;
             }
       }
       __syncthreads();
       // 16 lanes per output row (one DPP row), each taking 16-byte chunks c and c + 16
 #pragma unroll 2
       for (int i = 0; i < kOutTokens * (FM / 16) / kThreads; ++i) {
-        const int ci = i * kThreads + tid;
+        const int ci = i * kThreads + etid;
         const int row = ci >> 4, c = ci & 15;
         const int tk = half * kOutTokens + row;   // token within the tile
         const int64_t t = t0 + tk;
@@ -375,7 +425,7 @@ void fp8_head_kernel(Fp8Params p) {
           const int64_t v = v0 + chunk * 8;
           in[h] = t < p.n && v < p.v;
           const u32x4_t x =
-              *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + row * kOutRow + chunk * 16);
+              *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + kOutOff + row * kOutRow + chunk * 16);
           if (in[h]) *reinterpret_cast<uint4*>(p.out + t * p.ldo + v) = make_uint4(x[0], x[1], x[2], x[3]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -411,6 +461,13 @@ void fp8_head_kernel(Fp8Params p) {
         }
       }
       __syncthreads();
+    }
+    staged = pf;
+    if (pf) {   // the next tile's first fragments (landed before the epilogue), then its
+                // stage-1 weight fills into buffer 1, free again after the epilogue's last barrier
+      read_frags();
+#pragma unroll
+      for (int i = 0; i < DmaTile<FM, kWaves>::NI; ++i) ta.issue(pan + kQBlock, buf(1), wv, i);
     }
   }
   if (p.part && tid < FN && t0 + tid < p.n) {
