@@ -69,6 +69,10 @@ def _assert_fp8_logits(got, x, codes, scale):
     (200, 384, 2048),
     (3072, 128, 16384),   # 12 token tiles: 64 splits in three rounds of 4 x 8 XCD blocks
     (300, 256, 1152),     # the last vocab tile half past V, the last token tile partial
+    # 16 splits of 2-3 vocab tiles: with 2 K blocks the next tile's first stage is prefetched
+    # (into the last tile, half past V); with 3 each tile starts with its own fills
+    (4096, 256, 10112),
+    (4096, 384, 10112),
 ])
 def test_fp8_linear_matches_oracle(gpu_lib, n, d, v):
     x, codes, scale = synthetic.fp8_teacher_inputs(n, d, v, 11 + n, DEV)
@@ -112,7 +116,7 @@ def _lse64(x):
     return (mx + np.log(np.exp(x - mx).sum(-1, keepdims=True)))[..., 0]
 
 
-@pytest.mark.parametrize("n,d,v", [(200, 384, 2048), (640, 256, 8192)])
+@pytest.mark.parametrize("n,d,v", [(200, 384, 2048), (640, 256, 8192), (4096, 256, 10112)])
 def test_fp8_teacher_lse_from_the_epilogue(gpu_lib, n, d, v):
     """The producer's log-sum-exp of each bf16 output row (train.py:280-290's teacher,
     C4's head): the same logits as fp8_linear, and their LSE in fp64 to 2e-6."""
