@@ -244,7 +244,8 @@ void fp8_head_kernel(Fp8Params p) {
     return p.ws + (int64_t)vb * KB;
   };
   DmaTile<FM, kWaves> ta;
-  bool staged = false;   // this tile's first stage in buffer 0, its fragments in registers
+  bool staged = false;   // this tile's first stage in buffer 0, its fragments in a / b and its
+                         // block scales in c_cur (set up by the previous tile)
   float c_cur[2], c_prev[2], xn[2], wnx;
   i32x8_t a[2];            // [kk]: block row q's A fragments, reloaded after their last use
   i32x8_t b[2][2];         // [j][kk]
@@ -270,9 +271,7 @@ void fp8_head_kernel(Fp8Params p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[q][j][e] = 0.f;
 
-    // prologue: stage 0's scales, then the fills of stage 0 and stage 1's A fills (its B
-    // fills go out in stage 0); wait for stage 0 only (vector-memory operations complete
-    // in order)
+    // the blocks carried into the first stage's folds start at zero (they add nothing)
     c_prev[0] = c_prev[1] = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -288,6 +287,9 @@ void fp8_head_kernel(Fp8Params p) {
       for (int kk = 0; kk < 2; ++kk) a[kk] = rd32(buf(0), wm * 128 + fr, kk * 4 + fkh * 2);
     };
     if (!staged) {
+      // prologue: stage 0's scales, then the fills of stage 0 and stage 1's A fills (its B
+      // fills go out in stage 0); wait for stage 0 only (vector-memory operations complete
+      // in order)
       tile_init_here(ta, p.ldw, v0, p.v, wv);
       {
         const float w0 = wsrow[0];
