@@ -403,6 +403,10 @@ def time_cpu(run, reps: int = 3):
     return statistics.median(times), times
 
 
+# CPU-baseline sample rows for the secondary lines that carry one (whole blocks of 8)
+SECONDARY_CPU_ROWS = {"c1": 512, "c4": 256}
+
+
 def cpu_report(rows, n, med, times, threads, what, extra=""):
     """The cpu_baseline object: slots/s of a whole-block sample.  Every [N, V] operation is
     row-local and accept_len is block-local, so the sample's rate is the full batch's rate."""
@@ -967,6 +971,10 @@ def main():
             r2 = measure(wl2, args, name)
             if "ceilings" in wl2:
                 r2["library_ceilings"] = wl2["ceilings"]()
+            # the oracle on the host beside the logit stream and the fp8 teacher head too, on
+            # smaller whole-block samples than the headline's (a few seconds each)
+            if not args.no_cpu_baseline and name in SECONDARY_CPU_ROWS:
+                r2["cpu_baseline"] = wl2["cpu_baseline"](SECONDARY_CPU_ROWS[name])
             r2["inputs_sha256"] = {k: sample_sha256(t) for k, t in wl2.get("inputs", {}).items() if t is not None}
             secondary[name] = r2
             del wl2
