@@ -182,21 +182,6 @@ __device__ __forceinline__ int lane_here() {
   return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, z));
 }
 
-// DmaTile::init with the lane formed in place (same offsets): the next tile's weight rows
-// are set up inside the stage loop.
-template <int ROWS, int WAVES>
-__device__ __forceinline__ void tile_init_here(DmaTile<ROWS, WAVES>& tt, int64_t ld_bytes, int64_t r0, int64_t rmax, int wv) {
-  const int lane = lane_here();
-#pragma unroll
-  for (int i = 0; i < DmaTile<ROWS, WAVES>::NI; ++i) {
-    const int row = (wv * DmaTile<ROWS, WAVES>::NI + i) * 8 + (lane >> 3);
-    int64_t rr = r0 + row;
-    rr = rr < rmax ? rr : rmax - 1;
-    const int chunk = (lane & 7) ^ swz(row);
-    tt.off[i] = (uint32_t)((rr - r0) * ld_bytes + chunk * 16);
-  }
-}
-
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fp8_head_kernel(Fp8Params p) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
@@ -290,7 +275,7 @@ void fp8_head_kernel(Fp8Params p) {
       // prologue: stage 0's scales, then the fills of stage 0 and stage 1's A fills (its B
       // fills go out in stage 0); wait for stage 0 only (vector-memory operations complete
       // in order)
-      tile_init_here(ta, p.ldw, v0, p.v, wv);
+      ta.init(p.ldw, v0, p.v, wv, lane_here());
       {
         const float w0 = wsrow[0];
         c_cur[0] = p.xs[xsoff[0]] * w0;
@@ -317,7 +302,7 @@ void fp8_head_kernel(Fp8Params p) {
       const int kn = more ? t + 1 : 0;              // the next stage: this tile's or the next tile's first
       const float* wsk = more ? wsrow : wsn;
       const bool fill_next = pf && t == KB - 2;     // slots 12-15 fill the next tile's first stage
-      if (fill_next) tile_init_here(ta, p.ldw, v0 + FM, p.v, wv);
+      if (fill_next) ta.init(p.ldw, v0 + FM, p.v, wv, lane_here());
       // 16 MFMA slots s = 4 q + 2 j + kk; the pair (q, j) accumulates over the stage's two
       // 64-K halves into part[j], which is folded into the accumulator with the block
       // scale in slot (q + 1, j, 0), before the next pair overwrites it (sched_barrier

@@ -67,7 +67,10 @@ struct DmaTile {
   uint32_t off[NI];  // per-lane byte offsets from the tile's first row, stage 0
   // ld_bytes: row pitch in bytes; r0: first row; rmax: rows in the matrix
   __device__ __forceinline__ void init(int64_t ld_bytes, int64_t r0, int64_t rmax, int wv) {
-    const int lane = threadIdx.x & 63;
+    init(ld_bytes, r0, rmax, wv, threadIdx.x & 63);
+  }
+  // the same with the lane's index in its wave given
+  __device__ __forceinline__ void init(int64_t ld_bytes, int64_t r0, int64_t rmax, int wv, int lane) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int row = (wv * NI + i) * 8 + (lane >> 3);
