@@ -145,6 +145,7 @@ def _assert_grads(dl, mk, g1, w1_grad, w2_grad, keep=None):
     (24, 4096, 128, 64, None),        # fewer tokens than one stage: the register path alone
     (1000, 4096, 128, 64, None),      # 31 stages (a partial unrolled group) plus an 8-token tail
     (128, 2048, 128, 512, 8),         # rank 512: two rank tiles in the w2.grad GEMM
+    (32768, 2048, 3072, 256, None),   # six rounds of dh tiles, one launch each, then the Markov tiles
 ])
 def test_markov_backward_matches_oracle(gpu_lib, n, v, d, r, id_range):
     dl, w, mk, g1 = _bwd_inputs(n, v, d, r, 60 + n, id_range)
