@@ -131,25 +131,48 @@ def _csv_rows(directory: str, suffix: str):
         return list(csv.DictReader(f))
 
 
+def _launches(counters, durations):
+    """Per-launch records from one pass's per-dispatch ones ({dispatch id: (kernel name,
+    {counter: value})} and {dispatch id: ns}).  A run of consecutive dispatches of one library
+    kernel is one launch: the library issues a long GEMM as one launch per round of
+    workgroups inside one timer scope (the dh GEMM past five rounds).  Its counters and
+    durations are summed.  Returns [(timer name, {counter: sum}, ns or None, dispatches)] for
+    the library kernels."""
+    out, prev = [], None
+    for d in sorted(counters):
+        kname, vals = counters[d]
+        name = timer_name(kname)
+        dur = durations.get(d)
+        if name is not None and name == prev:
+            _, acc, ns, k = out[-1]
+            for c, v in vals.items():
+                acc[c] = acc.get(c, 0.0) + v
+            out[-1] = (name, acc, None if ns is None or dur is None else ns + dur, k + 1)
+        elif name is not None:
+            out.append((name, dict(vals), dur, 1))
+        prev = name
+    return out
+
+
 def _counter_per_kernel(directory: str, counter: str):
-    """Median per-dispatch value (KiB) of `counter` for each library kernel, plus the
+    """Median per-launch value (KiB) of `counter` for each library kernel, plus the
     calibration kernel's value."""
     import statistics
 
-    per, calib = {}, []
-    rows = [r for r in _csv_rows(directory, "counter_collection.csv") if r["Counter_Name"] == counter]
-    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    counters, calib = {}, []
     seen_library = False   # the calibration kernel follows the driver's first step
-    for r in rows:
-        val = float(r["Counter_Value"])
-        name = timer_name(r["Kernel_Name"])
-        if name:
+    rows = [r for r in _csv_rows(directory, "counter_collection.csv") if r["Counter_Name"] == counter]
+    for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])):
+        counters[int(r["Dispatch_Id"])] = (r["Kernel_Name"], {counter: float(r["Counter_Value"])})
+        if timer_name(r["Kernel_Name"]):
             seen_library = True
-            per.setdefault(name, []).append(val)
         elif seen_library and "neg" in r["Kernel_Name"]:
-            calib.append(val)
+            calib.append(float(r["Counter_Value"]))
     if not calib:
         raise SystemExit(f"no calibration dispatch (torch.neg) in {directory}")
+    per = {}
+    for name, vals, _, _ in _launches(counters, {}):
+        per.setdefault(name, []).append(vals[counter])
     return {k: statistics.median(v) for k, v in per.items()}, max(calib)
 
 
@@ -165,7 +188,8 @@ def traffic_summary(fetch_dir: str, write_dir: str, config: str, command: str) -
            "Each counter pass runs `bench.py --pmc-driver`: one step, a torch fp32 negation of 1 GiB into another "
            "1 GiB (the calibration kernel), then two steps. The calibration kernel reads "
            f"{fcal:.0f} KiB and writes {wcal:.0f} KiB by the counters, so FETCH_SIZE is scaled by "
-           f"{ff:.4f} and WRITE_SIZE by {wf:.4f}. Values are per-dispatch medians; FETCH_SIZE counts L2 fills "
+           f"{ff:.4f} and WRITE_SIZE by {wf:.4f}. Values are per-launch medians (a launch issued as one dispatch "
+           "per round of workgroups sums its dispatches); FETCH_SIZE counts L2 fills "
            "from the fabric, which include Infinity Cache (MALL) hits.", "",
            "| kernel | fetch GB | write GB | traffic GB |", "|---|---:|---:|---:|"]
     machine = []
@@ -180,10 +204,28 @@ def traffic_summary(fetch_dir: str, write_dir: str, config: str, command: str) -
 
 def stats_summary(directory: str, config: str, command: str) -> str:
     rows = _csv_rows(directory, "kernel_stats.csv")
+    # launches per kernel from the same run's kernel trace (a launch issued as one dispatch per
+    # round of workgroups counts once); the column appears only when they differ from calls
+    launches = {}
+    try:
+        trace = {int(r["Dispatch_Id"]): (r["Kernel_Name"], {}) for r in _csv_rows(directory, "kernel_trace.csv")}
+    except SystemExit:
+        trace = {}
+    for name, _, _, _ in _launches(trace, {}):
+        launches[name] = launches.get(name, 0) + 1
+    split = any(launches.get(timer_name(r["Name"]), int(r["Calls"])) != int(r["Calls"])
+                for r in rows if timer_name(r["Name"]))
+    head = "| kernel | timer name | calls | total ms | average ms | % of GPU time |"
+    rule = "|---|---|---:|---:|---:|---:|"
+    if split:
+        head = "| kernel | timer name | calls | launches | total ms | average ms per call | average ms per launch | % of GPU time |"
+        rule = "|---|---|---:|---:|---:|---:|---:|---:|"
     out = [f"# rocprofv3 kernel stats: {config.upper()}", "", "Command (from the repository root on the MI355X box):",
-           "", "```", command.strip(), "```", "",
-           "| kernel | timer name | calls | total ms | average ms | % of GPU time |",
-           "|---|---|---:|---:|---:|---:|"]
+           "", "```", command.strip(), "```", ""]
+    if split:
+        out += ["A launch is one timer scope of the library: the dh GEMM past five rounds of workgroups is "
+                "issued as one dispatch per round, so its calls are several per launch.", ""]
+    out += [head, rule]
     other = 0.0
     for r in rows:
         name = timer_name(r["Name"])
@@ -193,9 +235,16 @@ def stats_summary(directory: str, config: str, command: str) -> str:
         short = r["Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
         if len(short) > 90:
             short = short[:87] + "..."
-        out.append(f"| `{short}` | {name} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
-                   f"{float(r['AverageNs']) / 1e6:.4f} | {float(r['Percentage']):.1f} |")
-    out.append(f"| (torch input generation and copies, outside the timed steps) | | | | | {other:.1f} |")
+        total = float(r["TotalDurationNs"]) / 1e6
+        if split:
+            n_l = launches.get(name, int(r["Calls"]))
+            out.append(f"| `{short}` | {name} | {r['Calls']} | {n_l} | {total:.3f} | "
+                       f"{float(r['AverageNs']) / 1e6:.4f} | {total / max(n_l, 1):.4f} | {float(r['Percentage']):.1f} |")
+        else:
+            out.append(f"| `{short}` | {name} | {r['Calls']} | {total:.3f} | "
+                       f"{float(r['AverageNs']) / 1e6:.4f} | {float(r['Percentage']):.1f} |")
+    cols = "| | | | | | |" if split else "| | | | |"
+    out.append(f"| (torch input generation and copies, outside the timed steps) {cols} {other:.1f} |")
     out.append("")
     return "\n".join(out)
 
@@ -237,7 +286,7 @@ def _per_dispatch(directory: str):
 
 def mfma_summary(directory: str, config: str, command: str) -> str:
     """Markdown: the matrix cores of each library GEMM kernel from one rocprofv3 pass with
-    MFMA_COUNTERS and --kernel-trace (per-dispatch medians):
+    MFMA_COUNTERS and --kernel-trace (per-launch medians):
     * executed FLOP = MOPS x 512 (bf16 or fp8), to check against the algorithmic count;
     * clock = GRBM_GUI_ACTIVE / duration, where GRBM_GUI_ACTIVE is summed over the 8 XCDs
       (so it is divided by 8);
@@ -248,16 +297,15 @@ def mfma_summary(directory: str, config: str, command: str) -> str:
 
     counters, durations = _per_dispatch(directory)
     per = {}
-    for d, (kname, vals) in counters.items():
-        name = timer_name(kname)
-        if not name or d not in durations or not all(c in vals for c in MFMA_COUNTERS):
+    for name, vals, ns, _ in _launches(counters, durations):
+        if ns is None or not all(c in vals for c in MFMA_COUNTERS):
             continue
         bf, f8 = vals["SQ_INSTS_VALU_MFMA_MOPS_BF16"], vals["SQ_INSTS_VALU_MFMA_MOPS_F8"]
         if bf + f8 == 0:
             continue
         dtype = "fp8" if f8 > bf else "bf16"
         flop = 512.0 * (f8 if dtype == "fp8" else bf)
-        dur = durations[d] * 1e-9
+        dur = ns * 1e-9
         cycles = vals["GRBM_GUI_ACTIVE"] / 8.0
         per.setdefault(name, []).append(dict(
             dtype=dtype, flop=flop, ms=dur * 1e3, clock_GHz=cycles / dur / 1e9,
@@ -269,13 +317,14 @@ def mfma_summary(directory: str, config: str, command: str) -> str:
     out = [f"# Matrix cores per GEMM kernel: {config.upper()} (rocprofv3 MFMA counters)", "",
            "Command (from the repository root on the MI355X box):", "", "```", command.strip(), "```", "",
            "One `bench.py --pmc-driver` pass (one step, a calibration copy, two steps) with "
-           f"`--pmc {' '.join(MFMA_COUNTERS)} --kernel-trace`; per-dispatch medians. FLOP executed = "
+           f"`--pmc {' '.join(MFMA_COUNTERS)} --kernel-trace`; per-launch medians (a launch issued as one dispatch "
+           "per round of workgroups sums its dispatches' counters and durations). FLOP executed = "
            "`SQ_INSTS_VALU_MFMA_MOPS_*` x 512. Clock = `GRBM_GUI_ACTIVE` / 8 XCDs / kernel duration. "
            "MFMA busy = `SQ_VALU_MFMA_BUSY_CYCLES` / (cycles x 1024 SIMDs). Per-clock = FLOP / (cycles x 1024 "
            "SIMDs x dense FLOP per SIMD per clock: 1024 bf16, 2048 fp8), the fraction of the matrix cores' "
            "peak at the clock the chip ran. Peak fraction = FLOP / duration / (2.5 PFLOP/s bf16, 5.0 fp8), "
            "against the published 2.4 GHz figure.", "",
-           "| kernel | dtype | dispatches | duration ms | TFLOP executed | clock GHz | MFMA busy | per-clock | "
+           "| kernel | dtype | launches | duration ms | TFLOP executed | clock GHz | MFMA busy | per-clock | "
            "of dense peak |", "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
     machine = []
     for name in sorted(per):
@@ -319,7 +368,7 @@ CUS = 256                           # MI355X compute units (one L1 each)
 
 def memory_summary(directories, config: str, command: str) -> str:
     """Markdown: how each library GEMM kernel's loads move through the L1 (TCP) and the L2
-    (TCC), from the MEMORY_PASSES runs (per-dispatch medians, each pass's values taken
+    (TCC), from the MEMORY_PASSES runs (per-launch medians, each pass's values taken
     together):
     * L1 -> L2 read requests per launch, one per 128-byte line;
     * mean L2 read latency = TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ (cycles);
@@ -332,9 +381,8 @@ def memory_summary(directories, config: str, command: str) -> str:
     per = {}
     for directory in directories:
         counters, durations = _per_dispatch(directory)
-        for d, (kname, vals) in counters.items():
-            name = timer_name(kname)
-            if not name or "GRBM_GUI_ACTIVE" not in vals or d not in durations:
+        for name, vals, ns, _ in _launches(counters, durations):
+            if "GRBM_GUI_ACTIVE" not in vals or ns is None:
                 continue
             cycles = vals["GRBM_GUI_ACTIVE"] / 8.0
             row = {}
@@ -342,7 +390,7 @@ def memory_summary(directories, config: str, command: str) -> str:
                 req, lat = vals["TCP_TCC_READ_REQ_sum"], vals["TCP_TCC_READ_REQ_LATENCY_sum"]
                 row.update(req=req, latency=lat / req, inflight=lat / (cycles * CUS),
                            pending=vals["TCP_PENDING_STALL_CYCLES_sum"] / (cycles * CUS), cycles=cycles,
-                           ms=durations[d] / 1e6)
+                           ms=ns / 1e6)
             if "TCC_HIT_sum" in vals and vals["TCC_HIT_sum"] + vals["TCC_MISS_sum"] > 0:
                 row["hit"] = vals["TCC_HIT_sum"] / (vals["TCC_HIT_sum"] + vals["TCC_MISS_sum"])
             for k, v in row.items():
@@ -352,7 +400,8 @@ def memory_summary(directories, config: str, command: str) -> str:
     passes = "; ".join(f"`--pmc {' '.join(p)} --kernel-trace`" for p in MEMORY_PASSES)
     out = [f"# L1 and L2 read pipeline per kernel: {config.upper()} (rocprofv3 TCP / TCC counters)", "",
            "Commands (from the repository root on the MI355X box):", "", "```", command.strip(), "```", "",
-           f"One `bench.py --pmc-driver` pass per counter set ({passes}); per-dispatch medians. A request is one "
+           f"One `bench.py --pmc-driver` pass per counter set ({passes}); per-launch medians (a launch issued as "
+           "one dispatch per round of workgroups sums its dispatches). A request is one "
            "128-byte line from a CU's L1 (TCP) to the L2 (TCC). Latency = TCP_TCC_READ_REQ_LATENCY / "
            "TCP_TCC_READ_REQ, in cycles. Lines in flight per CU = TCP_TCC_READ_REQ_LATENCY / (cycles x 256 CUs), "
            "the mean number of outstanding L1 misses per CU (Little's law). Pending stall = "

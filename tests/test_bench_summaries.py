@@ -72,3 +72,65 @@ def test_mfma_summary_clock_and_busy(tmp_path):
     assert float(m["clock_GHz"]) == pytest.approx(1.5, abs=1e-3)
     assert float(m["mfma_busy"]) == pytest.approx(0.5, abs=1e-4)
     assert float(m["per_clock"]) == pytest.approx(0.4, abs=1e-4)
+
+
+DH = "void ns::(anonymous namespace)::dh_kernel(ns::(anonymous namespace)::BwdParams)"
+
+
+def test_launch_split_into_rounds_counts_once(tmp_path):
+    # two steps; each issues the dh GEMM as three dispatches (one per round) between other kernels:
+    # the traffic and matrix-core figures are per launch (sums over the three), not per dispatch
+    cycles = 1.0e6
+    def dh(d, k):
+        return (d, DH, 1_000_000, {"SQ_INSTS_VALU_MFMA_MOPS_BF16": 1.0e6 * k, "SQ_INSTS_VALU_MFMA_MOPS_F8": 0.0,
+                                   "SQ_VALU_MFMA_BUSY_CYCLES": 0.5 * cycles * 1024, "GRBM_GUI_ACTIVE": 8 * cycles})
+    step1 = [(1, HEAD, 2_000_000, {"SQ_INSTS_VALU_MFMA_MOPS_BF16": 5.0e6, "SQ_INSTS_VALU_MFMA_MOPS_F8": 0.0,
+                                   "SQ_VALU_MFMA_BUSY_CYCLES": 0.0, "GRBM_GUI_ACTIVE": 16 * cycles}),
+             dh(2, 1), dh(3, 2), dh(4, 3)]
+    step2 = [(5, OTHER, 1000, {"SQ_INSTS_VALU_MFMA_MOPS_BF16": 0.0, "SQ_INSTS_VALU_MFMA_MOPS_F8": 0.0,
+                               "SQ_VALU_MFMA_BUSY_CYCLES": 0.0, "GRBM_GUI_ACTIVE": 8.0}),
+             dh(6, 1), dh(7, 2), dh(8, 3)]
+    _write_pass(tmp_path / "m", step1 + step2)
+    text = bench.mfma_summary(str(tmp_path / "m"), "c3", "cmd")
+    m = _machine(text, "mfma", "dh_gemm")
+    assert float(m["flop"]) == pytest.approx(512 * 6.0e6)          # 1 + 2 + 3 million MOPS per launch
+    assert float(m["clock_GHz"]) == pytest.approx(1.0, abs=1e-3)   # 3e6 cycles over 3 ms
+    assert float(m["mfma_busy"]) == pytest.approx(0.5, abs=1e-4)
+    assert "| `dh_gemm` | bf16 | 2 | 3.000 |" in text                # two launches of 3 ms
+
+    # traffic: FETCH_SIZE per launch is the sum of its dispatches (KiB; calibration 1 GiB)
+    for sub, counter in (("f", "FETCH_SIZE"), ("w", "WRITE_SIZE")):
+        rows = [(1, HEAD, 10, {counter: 100.0}), (2, DH, 10, {counter: 10.0}), (3, DH, 10, {counter: 20.0}),
+                (4, OTHER, 10, {counter: 1024.0 * 1024.0}), (5, DH, 10, {counter: 30.0}),
+                (6, DH, 10, {counter: 30.0}), (7, HEAD, 10, {counter: 100.0})]
+        _write_pass(tmp_path / sub, rows)
+    text = bench.traffic_summary(str(tmp_path / "f"), str(tmp_path / "w"), "c3", "cmd")
+    t = _machine(text, "traffic", "dh_gemm")
+    # launches of 30 and 60 KiB: median 45 KiB
+    assert float(t["fetch_bytes"]) == pytest.approx(45 * 1024)
+    assert float(t["write_bytes"]) == pytest.approx(45 * 1024)
+    assert float(_machine(text, "traffic", "head_stats")["fetch_bytes"]) == pytest.approx(100 * 1024)
+
+
+def test_stats_summary_launch_column(tmp_path):
+    d = tmp_path / "s"
+    os.makedirs(d)
+    with open(d / "run_kernel_stats.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
+        w.writerow([DH, 6, 60_000_000, 10_000_000, 60.0])
+        w.writerow([HEAD, 2, 40_000_000, 20_000_000, 40.0])
+    _write_pass(d, [(1, HEAD, 1, {}), (2, DH, 1, {}), (3, DH, 1, {}), (4, DH, 1, {}),
+                    (5, HEAD, 1, {}), (6, DH, 1, {}), (7, DH, 1, {}), (8, DH, 1, {})])
+    text = bench.stats_summary(str(d), "c3", "cmd")
+    assert "| dh_gemm | 6 | 2 | 60.000 | 10.0000 | 30.0000 | 60.0 |" in text
+    assert "| head_stats | 2 | 2 | 40.000 | 20.0000 | 20.0000 | 40.0 |" in text
+    # one dispatch per launch everywhere: the plain table
+    os.remove(d / "run_kernel_trace.csv")
+    _write_pass(d, [(1, HEAD, 1, {}), (2, DH, 1, {}), (3, OTHER, 1, {}), (4, HEAD, 1, {}), (5, DH, 1, {})])
+    with open(d / "run_kernel_stats.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
+        w.writerow([DH, 2, 20_000_000, 10_000_000, 50.0])
+    text = bench.stats_summary(str(d), "c2", "cmd")
+    assert "| dh_gemm | 2 | 20.000 | 10.0000 | 50.0 |" in text
