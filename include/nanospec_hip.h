@@ -303,6 +303,12 @@ typedef struct {
 int ns_profile_begin(void);
 int ns_profile_end(ns_kernel_time* out, int capacity, int* count);
 
+/* Restricts the timing to launches whose timer name is in `names` (comma-separated,
+ * e.g. "head_stats,head_emit"); NULL or "" times every launch.  The other launches run
+ * without events, so a timed window is not lengthened by events around short kernels.
+ * Applies from the next launch until changed. */
+int ns_profile_select(const char* names);
+
 #ifdef __cplusplus
 }
 #endif

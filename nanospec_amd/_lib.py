@@ -111,6 +111,7 @@ class KernelTime(ctypes.Structure):
 
 
 SIGNATURES["ns_profile_begin"] = ([], _I)
+SIGNATURES["ns_profile_select"] = ([ctypes.c_char_p], _I)
 SIGNATURES["ns_profile_end"] = ([ctypes.POINTER(KernelTime), _I, ctypes.POINTER(_I)], _I)
 
 _lib = None
@@ -221,17 +222,26 @@ def scale_inplace(t: torch.Tensor, factor: float) -> None:
 
 class KernelTimer:
     """Context manager around ns_profile_begin/end: per-kernel launches and
-    total milliseconds, measured with HIP events on each launch's stream."""
+    total milliseconds, measured with HIP events on each launch's stream.
+    ``only``: the timer names to time (the others run without events); None: all."""
+
+    def __init__(self, only=None):
+        self.only = only
 
     def __enter__(self):
-        check(load().ns_profile_begin(), "ns_profile_begin")
+        lib = load()
+        names = ",".join(sorted(self.only)) if self.only else ""
+        check(lib.ns_profile_select(names.encode()), "ns_profile_select")
+        check(lib.ns_profile_begin(), "ns_profile_begin")
         self.times = {}
         return self
 
     def __exit__(self, *exc):
         buf = (KernelTime * 64)()
         count = _c.c_int(0)
-        status = load().ns_profile_end(buf, 64, _c.byref(count))
+        lib = load()
+        status = lib.ns_profile_end(buf, 64, _c.byref(count))
+        lib.ns_profile_select(b"")
         for i in range(min(count.value, 64)):
             name = buf[i].name.decode()
             self.times[name] = (buf[i].launches, buf[i].total_ms)

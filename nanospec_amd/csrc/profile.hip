@@ -24,6 +24,8 @@ std::mutex g_mu;
 std::atomic<bool> g_on{false};
 std::vector<Record> g_records;
 std::vector<hipEvent_t> g_pool;
+// ns_profile_select: ",name1,name2," or empty (every launch timed)
+std::string g_only;
 
 hipEvent_t take_event() {
   if (!g_pool.empty()) {
@@ -43,6 +45,7 @@ bool profiling() { return g_on.load(std::memory_order_acquire); }
 void* profile_start(const char* name, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!g_on.load(std::memory_order_relaxed)) return nullptr;
+  if (!g_only.empty() && g_only.find("," + std::string(name) + ",") == std::string::npos) return nullptr;
   Record r{name, take_event(), take_event(), hipSuccess};
   if (!r.start || !r.stop || hipEventRecord(r.start, st) != hipSuccess) {
     if (r.start) g_pool.push_back(r.start);
@@ -63,6 +66,12 @@ void profile_stop(void* token, hipStream_t st) {
 }  // namespace ns
 
 extern "C" {
+
+int ns_profile_select(const char* names) {
+  std::lock_guard<std::mutex> lk(ns::g_mu);
+  ns::g_only = names && *names ? "," + std::string(names) + "," : std::string();
+  return NS_OK;
+}
 
 int ns_profile_begin(void) {
   std::lock_guard<std::mutex> lk(ns::g_mu);

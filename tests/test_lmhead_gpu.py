@@ -147,3 +147,21 @@ def test_deterministic(gpu_lib):
     assert torch.equal(dl1, dl2) and torch.equal(dh1, dh2)
     for f in FIELDS:
         assert torch.equal(getattr(m1, f), getattr(m2, f))
+
+
+def test_kernel_timer_times_only_the_selected_launches(gpu_lib):
+    """ns_profile_select: launches outside the named set run without events (bench.py's timed
+    window times only the kernels with a roofline); the selection ends with the timer."""
+    from nanospec_amd import _lib
+
+    hidden, weight, markov, teacher, slots = synthetic.c0(DEV)
+    o = Objective(block_size=8)
+    with _lib.KernelTimer(only={"head_stats", "head_emit"}) as kt:
+        head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
+        torch.cuda.synchronize()
+    assert set(kt.times) == {"head_stats", "head_emit"}
+    assert all(c == 1 and ms > 0 for c, ms in kt.times.values())
+    with _lib.KernelTimer() as kt:
+        head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
+        torch.cuda.synchronize()
+    assert {"head_stats", "merge_rows", "head_emit", "finalize_metrics"} <= set(kt.times)
