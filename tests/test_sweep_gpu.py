@@ -86,3 +86,65 @@ def test_head_random(gpu_lib, i):
     if fp32_teacher:
         teacher = teacher.float()
     _check_full(hidden, weight, mk if markov else None, teacher, slots, Objective(block_size=8, gamma=gamma))
+
+
+def _fp8_case(i):
+    r = np.random.default_rng(9000 + i)
+    return int(r.integers(1, 1300)), 128 * int(r.integers(1, 7)), 128 * int(r.integers(1, 120))
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_fp8_random(gpu_lib, i):
+    """fp8_linear against the oracle's fp8_linear bound, and the producer's row LSE against fp64."""
+    from nanospec_amd import ops
+    from test_fp8_gpu import _assert_fp8_logits, _lse64
+
+    n, d, v = _fp8_case(i)
+    x, codes, scale = synthetic.fp8_teacher_inputs(n, d, v, 9100 + i, DEV)
+    w8 = codes.view(torch.float8_e4m3fn)
+    plain = ops.fp8_linear(x, w8, scale)
+    spec = ops.fp8_teacher_logits(x, w8, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(spec.logits, plain)
+    _assert_fp8_logits(_np(plain), _np(x), codes.cpu().numpy(), scale.cpu().numpy())
+    np.testing.assert_allclose(_np(spec.lse), _lse64(_np(plain)), rtol=2e-6, atol=2e-6)
+
+
+def _markov_case(i):
+    r = np.random.default_rng(9500 + i)
+    return (8 * int(r.integers(1, 80)), 64 * int(r.integers(1, 6)), 8 * int(r.integers(8, 2000)),
+            64 * int(r.integers(1, 6)))
+
+
+@pytest.mark.parametrize("i", range(5))
+def test_markov_factored_random(gpu_lib, i):
+    """The factored Markov head (a second K segment of the head GEMM) forward and backward
+    against the fp64 oracle: metrics, lse_z, z at the label, dl, dh, W2.grad and W1.grad."""
+    from dh_bar import assert_dh_rows
+    from nanospec_amd import head
+    from oracle import objective_ref as ref
+    from test_markov_gpu import _assert_grads, _inputs, _oracle
+
+    n, d, v, r = _markov_case(i)
+    hidden, weight, teacher, slots, mk = _inputs(n, d, v, r, 9600 + i)
+    o = Objective(block_size=8)
+    m, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov=mk)
+    g1 = (1e-3 * torch.randn((v, r), generator=torch.Generator(device=DEV).manual_seed(i), device=DEV)).bfloat16()
+    w1_grad, w2_grad = g1.clone(), torch.full_like(g1, float("nan"))
+    dh, dl = head.lm_head_ce_kl_backward(saved, return_dlogits=True, markov_grads=(w1_grad, w2_grad))
+    torch.cuda.synchronize()
+    z, m_ref, rows, dl_ref = _oracle(hidden, weight, teacher, slots, mk, o)
+    got = {f: float(getattr(m, f)) for f in ("ce", "kl", "numerator", "denominator", "accept_len_sum",
+                                              "accept_len_total")}
+    for f, w in got.items():
+        assert w == pytest.approx(m_ref[f], rel=1e-4, abs=1e-6 * max(1.0, abs(m_ref[f]))), f
+    rs = _np(saved.row_stats)
+    np.testing.assert_allclose(rs[:, 0], rows["lse_z"], rtol=2e-6, atol=5e-5)
+    np.testing.assert_allclose(rs[:, 5], z[np.arange(n), slots.target_ids.reshape(-1).cpu().numpy()],
+                               rtol=1e-5, atol=1e-5)
+    dln = _np(dl).reshape(n, -1)
+    diff = np.abs(dln.astype(np.float64) - dl_ref)
+    assert np.all(diff <= np.abs(dl_ref) * 2.0 ** -7 + 2e-5 * np.abs(dl_ref).max(axis=-1, keepdims=True))
+    # the backward from the kernel's own dl: dh = dl . W_lm and the Markov gradients
+    assert_dh_rows(_np(dh).reshape(n, -1), ref.lm_head_backward(dln, _np(weight)))
+    _assert_grads(dl.reshape(n, -1), mk, g1, w1_grad, w2_grad)
