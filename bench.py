@@ -36,7 +36,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c4", "c2x"],
+    p.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c3s", "c4", "c2x"],
                    help="one workload alone; default: C2 (the headline), then C1, C3, C4 and C2X as secondary lines")
     p.add_argument("--no-secondary", action="store_true", help="default run: C2 only")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -101,11 +101,12 @@ KERNEL_NAMES = [
     (r"scale_kernel", "scale_gradient"),
     (r"fp8_quant_kernel", "fp8_quant"),
     (r"fp8_head_kernel", "fp8_head_gemm"),
+    (r"copy_rows_kernel", "copy_rows"),
     (r"prepare_kernel", "prepare_slots"),
 ]
 # profiles/<prefix>_traffic.md and <prefix>_kernel_stats.md: named for the kernels and workload
-PROFILE_PREFIX = {"c1": "stream_c1", "c2": "lmhead_c2", "c3": "lmhead_c3", "c4": "fp8_lmhead_c4",
-                  "c2x": "head_ext_c2x"}
+PROFILE_PREFIX = {"c1": "stream_c1", "c2": "lmhead_c2", "c3": "lmhead_c3", "c3s": "lmhead_c3s",
+                  "c4": "fp8_lmhead_c4", "c2x": "head_ext_c2x"}
 CALIBRATION_BYTES = 1 << 30   # the --pmc-driver calibration (fp32 negation): reads and writes 1 GiB
 
 
@@ -569,7 +570,8 @@ def workload_head(device, args, which):
     from nanospec_amd import head, synthetic
     from nanospec_amd.config import Objective
 
-    gamma = 2.0 if which == "c3" else 4.0
+    gamma = 2.0 if which in ("c3", "c3s") else 4.0
+    skip = which == "c3s"
     fp8 = None
     if which == "c4":
         from nanospec_amd import ops
@@ -589,12 +591,19 @@ def workload_head(device, args, which):
             # the fp8 head also forms each teacher row's log-sum-exp, so pass 1 reads no teacher
             xt, codes, scale = fp8
             u = ops.fp8_teacher_logits(xt, codes.view(torch.float8_e4m3fn), scale)
-        metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, u, slots, o, markov_logits=markov)
+        metrics, saved = head.lm_head_ce_kl_loss(hidden, weight, u, slots, o, markov_logits=markov,
+                                                 skip_masked_rows=skip)
         dh = head.lm_head_ce_kl_backward(saved)
         return metrics, dh
 
     gemm = 2.0 * n * v * d
     kernel_flops = {"head_stats": gemm, "head_emit": gemm, "dh_gemm": gemm}
+    rows2 = n
+    if skip:
+        # pass 2 and the dh GEMM run on the rows whose dl is not all zero: here the supervised
+        # ones (every row's statistics are finite); their executed work, not N's
+        rows2 = int(((slots.valid.reshape(-1) != 0) | (slots.weights.reshape(-1) != 0)).sum())
+        kernel_flops = {"head_stats": gemm, "head_emit": 2.0 * rows2 * v * d, "dh_gemm": 2.0 * rows2 * v * d}
     kernel_fp8_flops = {"fp8_head_gemm": gemm} if fp8 is not None else {}
     # byte streams of the epilogues (for the per-kernel GB/s report): pass 1 reads
     # Markov + teacher, pass 2 also writes dl; the dh GEMM reads dl
@@ -648,10 +657,14 @@ def workload_head(device, args, which):
                           f"{'fp8_linear teacher head, ' if fp8 is not None else ''}LM-head GEMM (BLAS), "
                           f"ce_kl_loss, ce_kl_backward, dh GEMM; d={d}, V={v}; {threads} threads", extra)
 
-    name = {"c2": "C2 full fused", "c3": "C3 long-batch", "c4": "C4 FP8 teacher head + full fused"}[which]
+    name = {"c2": "C2 full fused", "c3": "C3 long-batch", "c4": "C4 FP8 teacher head + full fused",
+            "c3s": "C3 long-batch, pass 2 and dhidden on the rows with a nonzero dl only"}[which]
     config = {"workload": f"{name}: LM-head GEMM + Markov addend + CE+KL+accept fwd, dl + dhidden bwd",
               "N": n, "d": d, "V": v, "K": 8, "gamma": gamma, "global_batch": n, "seq_len": None,
               "parallelism": "single GPU"}
+    if skip:
+        config["skip_masked_rows"] = True
+        config["pass2_rows"] = rows2
     def ceilings():
         # the vendor library's plain GEMM of the same shape (hipBLASLt through torch.mm):
         # the logits GEMM without any objective work, output written to HBM
@@ -664,7 +677,9 @@ def workload_head(device, args, which):
             out["fp8"] = fp8_ceilings(fp8)
         return out
 
+    executed = gemm + 4.0 * rows2 * v * d if skip else None   # pass 1 on N rows, pass 2 and dh on rows2
     return dict(step=step, n=n, per_slot_bytes=None, per_slot_flops=4.0 * v * d, kernel_bytes=kernel_bytes,
+                executed_flops_per_step=executed,
                 kernel_flops=kernel_flops, kernel_fp8_flops=kernel_fp8_flops, cpu_baseline=cpu_baseline,
                 config=config, dtype="bf16" if fp8 is None else "bf16+fp8", ceilings=ceilings,
                 per_slot_fp8_flops=2.0 * v * d if fp8 is not None else None,
@@ -778,6 +793,7 @@ WORKLOADS = {
     "c2x": workload_c2x,
     "c2": lambda dev, a: workload_head(dev, a, "c2"),
     "c3": lambda dev, a: workload_head(dev, a, "c3"),
+    "c3s": lambda dev, a: workload_head(dev, a, "c3s"),
     "c4": lambda dev, a: workload_head(dev, a, "c4"),
 }
 
@@ -966,6 +982,10 @@ def measure(wl, args, config_name):
         if wl.get("per_slot_fp8_flops"):
             ideal_s += wl["per_slot_fp8_flops"] * n / (FP8_PEAK_TFLOPS * 1e12)
         step_roof["mfma_frac"] = ideal_s / (ms_per_step / 1e3)
+    if wl.get("executed_flops_per_step"):
+        # the work the step runs when it skips rows (c3s): below N's algorithmic work
+        step_roof["executed_TFLOPs"] = wl["executed_flops_per_step"] / (ms_per_step / 1e3) / 1e12
+        step_roof["executed_mfma_frac"] = step_roof["executed_TFLOPs"] / BF16_PEAK_TFLOPS
     out = {"value": value, "unit": "slots/s", "steps": args.steps, "warmup": args.warmup, "warmup_steps_run": warm,
            "ms_per_step": ms_per_step, "dtype": wl["dtype"], "config": wl["config"], "roofline": roof,
            "step_roofline": step_roof, "kernels": kernels, "wall_s": wall}
@@ -1028,10 +1048,10 @@ def main():
     # (C2 with final_norm, the factored Markov head and the pooled tail)
     secondary = {}
     if args.config is None and not args.no_secondary:
-        for name in ("c1", "c3", "c4", "c2x"):
+        for name in ("c1", "c3", "c3s", "c4", "c2x"):
             wl2 = WORKLOADS[name](device, args)
             r2 = measure(wl2, args, name)
-            if "ceilings" in wl2:
+            if "ceilings" in wl2 and name != "c3s":   # c3s: the same shapes as c3
                 r2["library_ceilings"] = wl2["ceilings"]()
             # the oracle on the host beside the logit stream and the fp8 teacher head too, on
             # smaller whole-block samples than the headline's (a few seconds each)

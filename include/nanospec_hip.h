@@ -140,6 +140,40 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
                         float inv_acc, void* dl, int64_t ldd, float* row_stats, float* metrics, void* workspace,
                         size_t workspace_bytes, ns_stream_t stream);
 
+/* The fused forward in two parts, for a caller that runs pass 2 on a subset of its rows:
+ * head.lm_head_ce_kl_loss(skip_masked_rows=True) runs pass 1 on every row, then pass 2 and
+ * the dh GEMM only on the rows whose dl is not all zero (supervised rows, and unsupervised
+ * rows whose log-normalisers are not finite), gathered with ns_copy_rows.  No counterpart in
+ * the reference: objective.py:49-67 in steps.
+ *   NS_PART_STATS: pass 1 and the merge; writes row_stats' lse_z, lse_u, ce, kl and z_label
+ *                  (dl is ignored).
+ *   NS_PART_EMIT:  pass 2 from row_stats' log-normalisers; writes dl (when not NULL) and the
+ *                  accept rate (with teacher-LSE args also kl) into row_stats.
+ * Arguments as ns_lmhead_ce_kl_fwd (labels, weights [n]; no valid, no metrics: those come from
+ * ns_objective_metrics over every row).  Workspace NS_WS_LMHEAD for n rows. */
+#define NS_PART_STATS 1
+#define NS_PART_EMIT 2
+int ns_lmhead_ce_kl_fwd_part(int part, const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                             const void* markov, int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
+                             const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,
+                             int64_t n, int64_t d, int64_t v, float c_ce, float c_kl, float inv_acc, void* dl,
+                             int64_t ldd, float* row_stats, void* workspace, size_t workspace_bytes,
+                             ns_stream_t stream);
+
+/* The six LossMetrics from complete row statistics [n, 8] (objective.py:42-46, 53-60:
+ * weighted CE and KL sums, accept_len from (accept_rate * valid).cumprod over blocks of k),
+ * as the last step of ns_lmhead_ce_kl_fwd forms them. */
+int ns_objective_metrics(const float* row_stats, const float* weights, const uint8_t* valid, int64_t n, int64_t k,
+                         float c_ce, float c_kl, float* metrics, ns_stream_t stream);
+
+/* dst row r = src row map[r] (row_bytes bytes each) for r < n_dst, and zeros where map[r] is
+ * outside [0, n_src): the gather of the rows ns_lmhead_ce_kl_fwd_part runs pass 2 on, and the
+ * scatter of their dl and dh back among zero rows.  Pitches in bytes; row_bytes and pitches
+ * multiples of 4 (16-byte accesses when all are multiples of 16).  No counterpart in the
+ * reference. */
+int ns_copy_rows(const void* src, int64_t ld_src, int64_t n_src, const int64_t* map, int64_t n_dst, int64_t row_bytes,
+                 void* dst, int64_t ld_dst, ns_stream_t stream);
+
 /* ns_lmhead_ce_kl_fwd without a workspace argument, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Its scratch is a static device array of 16 MiB per GPU,

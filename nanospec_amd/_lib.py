@@ -21,6 +21,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))
 ABI_VERSION = 6
 NS_BF16, NS_F32 = 0, 1
 NS_WS_LOGITS, NS_WS_LMHEAD, NS_WS_LMHEAD_BWD, NS_WS_FP8 = 0, 1, 2, 3
+NS_PART_STATS, NS_PART_EMIT = 1, 2
 NS_WS_RMS_NORM_BWD, NS_WS_LMHEAD_NORM_BWD, NS_WS_TEACHER_LOGITS = 4, 5, 6
 
 _c = ctypes
@@ -62,6 +63,13 @@ SIGNATURES = {
         [_P, _I, _I64, _P, _I, _I64, _P, _P, _I64, _I64, _F, _F, _F, _P, _P, _I64, _P],
         _I,
     ),
+    "ns_lmhead_ce_kl_fwd_part": (
+        [_I, _P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _TEACH, _P, _P, _I64, _I64, _I64, _F, _F, _F,
+         _P, _I64, _P, _P, _SZ, _P],
+        _I,
+    ),
+    "ns_objective_metrics": ([_P, _P, _P, _I64, _I64, _F, _F, _P, _P], _I),
+    "ns_copy_rows": ([_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P], _I),
     "ns_lmhead_ce_kl_fwd": (
         [_P, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _TEACH, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F,
          _P, _I64, _P, _P, _P, _SZ, _P],
@@ -197,6 +205,16 @@ def rows_2d(t: torch.Tensor, cols: int) -> tuple[torch.Tensor, int]:
         t2 = t2.contiguous()
     ld = t2.stride(0) if t2.shape[0] > 1 else cols
     return t2, ld
+
+
+def copy_rows(src: torch.Tensor, rows_map: torch.Tensor, n_dst: int, out: torch.Tensor) -> torch.Tensor:
+    """out row r = src row rows_map[r], zeros where rows_map[r] is outside [0, src rows)
+    (ns_copy_rows); src and out [rows, cols] views with unit column stride, the same dtype."""
+    row_bytes = src.shape[1] * src.element_size()
+    status = load().ns_copy_rows(ptr(src), src.stride(0) * src.element_size(), src.shape[0], ptr(rows_map), n_dst,
+                                 row_bytes, ptr(out), out.stride(0) * out.element_size(), stream(src.device))
+    check(status, "ns_copy_rows")
+    return out
 
 
 def pow2_ratio(emitted: int, wanted: int):

@@ -148,19 +148,27 @@ int ns_ce_kl_logits_bwd(const void* z, int z_dtype, int64_t ldz, const void* u, 
 
 namespace {
 
-// Validation shared by the fused forward and the dl re-emission (dense Markov addend or
-// factors).  `reemit`: dl is required, row_stats is an input, metrics and valid are unused.
+// What check_head_inputs requires besides the head's inputs.
+enum HeadCheck {
+  kCheckForward,   // valid, metrics and row_stats; dl optional
+  kCheckReemit,    // dl and row_stats (an input); metrics and valid unused
+  kCheckParts,     // row_stats; dl optional; metrics and valid unused
+};
+
+// Validation shared by the fused forward, its parts and the dl re-emission (dense Markov
+// addend or factors).
 int check_head_inputs(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
                       int64_t ldm, const ns::MarkovFactors* factors, const void* teacher, int t_dtype, int64_t ldt,
                       const ns_teacher_args* targs, const int64_t* labels, const float* weights,
                       const uint8_t* valid, int64_t n, int64_t d, int64_t v, int64_t k, const void* dl, int64_t ldd,
                       const float* row_stats, const float* metrics, const void* workspace, size_t workspace_bytes,
-                      bool reemit, int64_t* nt_out) {
+                      HeadCheck mode, int64_t* nt_out) {
+  const bool reemit = mode == kCheckReemit;
   if (!dtype_ok(t_dtype)) return fail(NS_EDTYPE, "unsupported teacher dtype code %d", t_dtype);
   if (v < 8 || v % 8) return fail(NS_EINVAL, "vocabulary size must be a positive multiple of 8 (got %lld)", (long long)v);
   if (d < 64 || d % 64) return fail(NS_EINVAL, "hidden size must be a positive multiple of 64 (got %lld)", (long long)d);
   int rc;
-  if ((rc = check_slots(labels, weights, valid, n, k, !reemit))) return rc;
+  if ((rc = check_slots(labels, weights, valid, n, k, mode == kCheckForward))) return rc;
   if ((rc = check_matrix(hidden, n, d, ldh, "hidden"))) return rc;
   if ((rc = check_matrix(weight, v, d, ldw, "weight"))) return rc;
   if (markov && (rc = check_matrix(markov, n, v, ldm, "markov"))) return rc;
@@ -172,8 +180,8 @@ int check_head_inputs(const void* hidden, int64_t ldh, const void* weight, int64
     return fail(NS_EINVAL, "teacher n_rows %lld without rows must equal n", (long long)targs->n_rows);
   if ((rc = check_matrix(teacher, nt, v, ldt, "teacher"))) return rc;
   if ((reemit || dl) && (rc = check_matrix(dl, n, v, ldd, "dl"))) return rc;
-  if (reemit ? (n > 0 && !row_stats) : (!metrics || (n > 0 && !row_stats)))
-    return fail(NS_ENULL, reemit ? "row_stats must be non-NULL" : "metrics and row_stats must be non-NULL");
+  if (mode != kCheckForward ? (n > 0 && !row_stats) : (!metrics || (n > 0 && !row_stats)))
+    return fail(NS_ENULL, mode != kCheckForward ? "row_stats must be non-NULL" : "metrics and row_stats must be non-NULL");
   const int64_t tq = t_dtype == NS_BF16 ? 8 : 4;
   if (!aligned(hidden) || !aligned(weight) || !aligned(teacher) || (markov && !aligned(markov)) || (dl && !aligned(dl)) ||
       ldh % 8 || ldw % 8 || (markov && ldm % 8) || ldt % tq || (dl && ldd % 8))
@@ -207,7 +215,7 @@ int lmhead_fwd_checked(const void* hidden, int64_t ldh, const void* weight, int6
   int64_t nt = 0;
   const int rc = check_head_inputs(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, targs, labels,
                                    weights, valid, n, d, v, k, dl, ldd, row_stats, metrics, workspace, workspace_bytes,
-                                   false, &nt);
+                                   kCheckForward, &nt);
   if (rc) return rc;
   ns::SlotArgs a{labels, weights, valid, n, k, c_ce, c_kl, inv_acc};
   const ns::TeacherSpec ts{targs ? targs->rows : nullptr, nt, targs ? targs->lse : nullptr};
@@ -230,6 +238,53 @@ int ns_lmhead_ce_kl_fwd(const void* hidden, int64_t ldh, const void* weight, int
   return lmhead_fwd_checked(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, teacher_args,
                             labels, weights, valid, n, d, v, k, c_ce, c_kl, inv_acc, dl, ldd, row_stats, metrics,
                             workspace, workspace_bytes, stream, "ns_lmhead_ce_kl_fwd");
+}
+
+int ns_lmhead_ce_kl_fwd_part(int part, const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                             const void* markov, int64_t ldm, const void* teacher, int t_dtype, int64_t ldt,
+                             const ns_teacher_args* teacher_args, const int64_t* labels, const float* weights,
+                             int64_t n, int64_t d, int64_t v, float c_ce, float c_kl, float inv_acc, void* dl,
+                             int64_t ldd, float* row_stats, void* workspace, size_t workspace_bytes,
+                             ns_stream_t stream) {
+  if (part != NS_PART_STATS && part != NS_PART_EMIT) return fail(NS_EINVAL, "part must be NS_PART_STATS or NS_PART_EMIT");
+  if (part == NS_PART_STATS) dl = nullptr;
+  int64_t nt = 0;
+  const int rc = check_head_inputs(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, teacher_args,
+                                   labels, weights, nullptr, n, d, v, 1, dl, ldd, row_stats, nullptr, workspace,
+                                   workspace_bytes, kCheckParts, &nt);
+  if (rc) return rc;
+  ns::SlotArgs a{labels, weights, nullptr, n, 1, c_ce, c_kl, inv_acc};
+  const ns::TeacherSpec ts{teacher_args ? teacher_args->rows : nullptr, nt, teacher_args ? teacher_args->lse : nullptr};
+  return hip_status(ns::lmhead_forward(hidden, ldh, weight, ldw, markov, ldm, nullptr, teacher, t_dtype, ldt, d, v, a,
+                                       &ts, dl, ldd, row_stats, nullptr, workspace,
+                                       reinterpret_cast<hipStream_t>(stream),
+                                       part == NS_PART_STATS ? ns::kHeadStats : ns::kHeadEmit),
+                    "ns_lmhead_ce_kl_fwd_part");
+}
+
+int ns_objective_metrics(const float* row_stats, const float* weights, const uint8_t* valid, int64_t n, int64_t k,
+                         float c_ce, float c_kl, float* metrics, ns_stream_t stream) {
+  if (n < 0) return fail(NS_EINVAL, "n must be >= 0 (got %lld)", (long long)n);
+  if (k < 1 || n % k) return fail(NS_EINVAL, "n (%lld) must be a multiple of the block size k (%lld >= 1)", (long long)n, (long long)k);
+  if (!metrics || (n > 0 && (!row_stats || !weights || !valid)))
+    return fail(NS_ENULL, "row_stats, weights, valid and metrics must be non-NULL");
+  ns::SlotArgs a{nullptr, weights, valid, n, k, c_ce, c_kl, 1.f};
+  return hip_status(ns::launch_finalize(nullptr, 1, a, const_cast<float*>(row_stats), metrics,
+                                        reinterpret_cast<hipStream_t>(stream)),
+                    "ns_objective_metrics");
+}
+
+int ns_copy_rows(const void* src, int64_t ld_src, int64_t n_src, const int64_t* map, int64_t n_dst, int64_t row_bytes,
+                 void* dst, int64_t ld_dst, ns_stream_t stream) {
+  if (n_src < 0 || n_dst < 0 || row_bytes < 0) return fail(NS_EINVAL, "row counts and row_bytes must be >= 0");
+  if (row_bytes % 4 || ld_src % 4 || ld_dst % 4 || ld_src < row_bytes || ld_dst < row_bytes)
+    return fail(NS_EINVAL, "row_bytes and the pitches must be multiples of 4 with pitches >= row_bytes");
+  if (n_dst > 0 && row_bytes > 0 && (!map || !dst || (n_src > 0 && !src))) return fail(NS_ENULL, "src, map and dst must be non-NULL");
+  if ((reinterpret_cast<uintptr_t>(src) & 3u) || (reinterpret_cast<uintptr_t>(dst) & 3u))
+    return fail(NS_EALIGN, "src and dst need 4-byte aligned base pointers");
+  return hip_status(ns::copy_rows(src, ld_src, n_src, map, n_dst, row_bytes, dst, ld_dst,
+                                  reinterpret_cast<hipStream_t>(stream)),
+                    "ns_copy_rows");
 }
 
 }  // extern "C"
@@ -322,7 +377,7 @@ int ns_lmhead_ce_kl_bwd(const void* hidden, int64_t ldh, const void* weight, int
   int64_t nt = 0;
   const int rc = check_head_inputs(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, t_dtype, ldt, teacher_args,
                                    labels, weights, nullptr, n, d, v, 1, dl, ldd, row_stats, nullptr, workspace,
-                                   workspace_bytes, true, &nt);
+                                   workspace_bytes, kCheckReemit, &nt);
   if (rc) return rc;
   ns::SlotArgs a{labels, weights, nullptr, n, 1, c_ce, c_kl, inv_acc};
   const ns::TeacherSpec ts{teacher_args ? teacher_args->rows : nullptr, nt, teacher_args ? teacher_args->lse : nullptr};

@@ -1173,7 +1173,7 @@ struct BwdParams {
   int mt, ct, ksplit;      // token tiles, d tiles, K splits
   int xa, xb;              // XCD block: xa token tiles x xb d tiles per round (0 = unblocked)
   int kt_total;            // ceil(V / BK)
-  int grid_main;           // mt * ct * ksplit workgroups of dh tiles
+  int grid_main;           // mt * ct * ksplit workgroups of dh tiles (padded to whole rounds)
   float* part;             // [ksplit][N][d] fp32
   // Markov extension (r > 0): workgroups past grid_main take mt x ct2 column tiles of
   // w2 [V, r] with their own K split count ksplit2, into part2 [ksplit2][N][r]
@@ -1218,6 +1218,7 @@ void dh_kernel(BwdParams p) {
     mt = (blk % gm) * p.xa + r % p.xa;
     ct = ((blk / gm) % gc) * p.xb + r / p.xa;
     ks = blk / (gm * gc);
+    if (ks >= nsplit) return;   // a block past the last (the grid is padded to whole rounds)
   } else {
     int L = g;
     if (G % kNumXcd == 0) L = (L % kNumXcd) * (G / kNumXcd) + L / kNumXcd;
@@ -1380,14 +1381,35 @@ BwdPlan bwd_plan(int64_t n, int64_t v, int64_t d, int64_t r = 0) {
     pl.grid += tiles2 * ks2;
   }
   // XCD block (dh_kernel's tile order): xa * xb = CUs per XCD, xa | mt, xb | ct, whole
-  // rounds on every XCD; the smallest xa + xb
+  // rounds on every XCD; the smallest xa + xb.  Failing whole rounds, the grid of blocks is
+  // padded to them (the workgroups past the last block return at once) when that adds at most
+  // an eighth: blocked, a K stage reads xa + xb operand tiles through an XCD's L2, against up to
+  // C unblocked.
   pl.xa = pl.xb = 0;
   if (cus % kNumXcd == 0) {
     const int C = cus / kNumXcd;
-    for (int a = 1; a <= C; ++a) {
-      const int b = C / a;
-      if (C % a || pl.mt % a || pl.ct % b || pl.grid_main % (kNumXcd * C)) continue;
-      if (pl.xa == 0 || a + b < pl.xa + pl.xb) { pl.xa = a; pl.xb = b; }
+    int pad_main = 0;
+    for (int pass = 0; pass < 2 && pl.xa == 0; ++pass) {
+      for (int a = 1; a <= C; ++a) {
+        const int b = C / a;
+        if (C % a || pl.mt % a || pl.ct % b) continue;
+        int g_main = pl.grid_main;
+        if (g_main % (kNumXcd * C)) {
+          if (pass == 0) continue;
+          const int64_t blocks = (int64_t)(pl.mt / a) * (pl.ct / b) * pl.ksplit;
+          g_main = (int)((blocks + kNumXcd - 1) / kNumXcd * kNumXcd * C);
+          if ((int64_t)g_main * 8 > (int64_t)pl.grid_main * 9) continue;
+        }
+        if (pl.xa == 0 || a + b < pl.xa + pl.xb || (a + b == pl.xa + pl.xb && g_main < pad_main)) {
+          pl.xa = a;
+          pl.xb = b;
+          pad_main = g_main;
+        }
+      }
+    }
+    if (pl.xa > 0 && pad_main != pl.grid_main) {
+      pl.grid += pad_main - pl.grid_main;
+      pl.grid_main = pad_main;
     }
   }
   return pl;
@@ -1410,12 +1432,15 @@ hipError_t launch_head(const HeadParams& p, int grid, hipStream_t st, const char
 
 template <typename TT, int FLAGS>
 hipError_t head_forward_typed(HeadParams& p, const HeadPlan& pl, const SlotArgs& a, float* row_stats,
-                              float* metrics, const HeadWs& w, hipStream_t st) {
-  hipError_t e = launch_head<MODE_STATS, TT, FLAGS>(p, pl.grid, st, "head_stats");
-  if (e != hipSuccess) return e;
-  const TeacherSpec tl{p.trows, p.nt, p.tlse};
-  if ((e = launch_merge(w.part1, w.zy, p.v, pl.splits, a, row_stats, st, p.tlse ? &tl : nullptr)) != hipSuccess)
-    return e;
+                              float* metrics, const HeadWs& w, hipStream_t st, int parts) {
+  hipError_t e;
+  if (parts & kHeadStats) {
+    if ((e = launch_head<MODE_STATS, TT, FLAGS>(p, pl.grid, st, "head_stats")) != hipSuccess) return e;
+    const TeacherSpec tl{p.trows, p.nt, p.tlse};
+    if ((e = launch_merge(w.part1, w.zy, p.v, pl.splits, a, row_stats, st, p.tlse ? &tl : nullptr)) != hipSuccess)
+      return e;
+  }
+  if (!(parts & kHeadEmit)) return hipSuccess;
   p.row_stats = row_stats;
   if ((e = launch_head<MODE_EMIT, TT, FLAGS>(p, pl.grid, st, "head_emit")) != hipSuccess) return e;
   return launch_finalize(w.parta, pl.splits, a, row_stats, metrics, st, p.tlse ? w.partk : nullptr);
@@ -1476,18 +1501,18 @@ HeadParams head_params(const void* hidden, int64_t ldh, const void* weight, int6
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,
                           int64_t ldm, const MarkovFactors* factors, const void* teacher, int tdt, int64_t ldt,
                           int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts, void* dl, int64_t ldd,
-                          float* row_stats, float* metrics, void* ws, hipStream_t st) {
-  if (a.n == 0) return launch_finalize(nullptr, 1, a, row_stats, metrics, st);
+                          float* row_stats, float* metrics, void* ws, hipStream_t st, int parts) {
+  if (a.n == 0) return metrics ? launch_finalize(nullptr, 1, a, row_stats, metrics, st) : hipSuccess;
   const HeadPlan pl = head_plan(a.n, v);
   HeadWs w;
   head_ws_layout(a.n, v, ws, &w);
   HeadParams p = head_params(hidden, ldh, weight, ldw, markov, ldm, factors, teacher, ldt, d, v, a, ts, dl, ldd, pl, w);
   if (p.tlse) {
-    if (tdt == kBF16) return head_forward_typed<uint16_t, kTeacherLse>(p, pl, a, row_stats, metrics, w, st);
-    return head_forward_typed<float, kTeacherLse>(p, pl, a, row_stats, metrics, w, st);
+    if (tdt == kBF16) return head_forward_typed<uint16_t, kTeacherLse>(p, pl, a, row_stats, metrics, w, st, parts);
+    return head_forward_typed<float, kTeacherLse>(p, pl, a, row_stats, metrics, w, st, parts);
   }
-  if (tdt == kBF16) return head_forward_typed<uint16_t, 0>(p, pl, a, row_stats, metrics, w, st);
-  return head_forward_typed<float, 0>(p, pl, a, row_stats, metrics, w, st);
+  if (tdt == kBF16) return head_forward_typed<uint16_t, 0>(p, pl, a, row_stats, metrics, w, st, parts);
+  return head_forward_typed<float, 0>(p, pl, a, row_stats, metrics, w, st, parts);
 }
 
 hipError_t lmhead_emit_dlogits(const void* hidden, int64_t ldh, const void* weight, int64_t ldw, const void* markov,

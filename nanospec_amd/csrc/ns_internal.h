@@ -46,7 +46,8 @@ struct TeacherSpec {
 hipError_t launch_merge(const RowPart* part1, const float* zy, int64_t v, int splits, const SlotArgs& a,
                         float* row_stats, hipStream_t st, const TeacherSpec* ts = nullptr);
 // Sum accept partials parta[N][S], form block lengths and the six metrics; with partk
-// (pass-2 sums of t (u - z)), KL = sum partk - lse_u + lse_z first.
+// (pass-2 sums of t (u - z)), KL = sum partk - lse_u + lse_z first.  parta NULL: the metrics
+// alone, from complete row_stats; metrics NULL: the row sums alone.
 hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, float* row_stats,
                            float* metrics, hipStream_t st, const float* partk = nullptr);
 // lse[t] = log-sum-exp from (max, sum-exp) partials part1[N][S] (mz, sz), fixed order.
@@ -86,10 +87,18 @@ size_t lmhead_workspace_bytes(int64_t n, int64_t v, int64_t d);
 // Raises the dynamic-LDS limit of every head instantiation lmhead_forward can launch, on the
 // current device (done lazily at launch otherwise; this lets a caller do it before capture).
 hipError_t lmhead_forward_prepare();
+// lmhead_forward's parts: pass 1 and the merge (row_stats' log-normalisers, CE, KL, z_label),
+// then pass 2 with the per-row accept (and teacher-once KL) sums and, when metrics is not
+// NULL, the metrics
+constexpr int kHeadStats = 1, kHeadEmit = 2, kHeadParts = kHeadStats | kHeadEmit;
 hipError_t lmhead_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
                           const void* markov, int64_t ldm, const MarkovFactors* factors, const void* teacher,
                           int tdt, int64_t ldt, int64_t d, int64_t v, const SlotArgs& a, const TeacherSpec* ts,
-                          void* dl, int64_t ldd, float* row_stats, float* metrics, void* ws, hipStream_t st);
+                          void* dl, int64_t ldd, float* row_stats, float* metrics, void* ws, hipStream_t st,
+                          int parts = kHeadParts);
+// dst row r = src row map[r] (row_bytes bytes), or zeros where map[r] is outside [0, n_src)
+hipError_t copy_rows(const void* src, int64_t ld_src, int64_t n_src, const int64_t* map, int64_t n_dst,
+                     int64_t row_bytes, void* dst, int64_t ld_dst, hipStream_t st);
 // Pass 2 of lmhead_forward alone: dl for a.inv_acc from the row_stats a forward over the
 // same inputs wrote (same kernel, so the same bits a forward with that inv_acc emits).
 // Workspace: lmhead_workspace_bytes.

@@ -413,6 +413,7 @@ hipError_t launch_finalize(const float* parta, int splits, const SlotArgs& a, fl
                        splits, a.n, row_stats);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   }
+  if (metrics == nullptr) return hipSuccess;   // the row sums alone (metrics formed later)
   NS_TIMED("finalize_metrics", st);
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kFinalThreads), 0, st, a.n, a.k, a.weights, a.valid, a.c_ce,
                      a.c_kl, row_stats, metrics);

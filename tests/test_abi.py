@@ -153,3 +153,31 @@ def test_workspace_query_degenerate_shapes(lib, kind, n, v, d):
     # divide by the number of row and column tiles, which is 0 here)
     assert lib.ns_workspace_bytes(kind, n, v, d) < 1 << 40
     assert lib.ns_lmhead_markov_bwd_workspace_bytes(n, v, d, 64) < 1 << 40
+
+
+def test_forward_parts_and_row_copy_validation(lib):
+    """The skip-masked-rows path's entry points reject bad arguments before device work."""
+    p = ctypes.c_void_p
+
+    def part(which, **over):
+        a = dict(hidden=256, teacher=256, labels=256, weights=256, n=8, d=64, v=64, dl=512, row_stats=256,
+                 ws=256, wsb=1 << 24)
+        a.update(over)
+        q = lambda x: None if x is None else p(x)
+        return lib.ns_lmhead_ce_kl_fwd_part(which, q(a["hidden"]), 64, p(256), 64, None, 64, q(a["teacher"]), 0, 64,
+                                            None, q(a["labels"]), q(a["weights"]), a["n"], a["d"], a["v"], 0.1, 0.9,
+                                            1.0, q(a["dl"]), 64, q(a["row_stats"]), q(a["ws"]), a["wsb"], None)
+
+    assert part(3) == -1 and "NS_PART" in lib.ns_last_error().decode()
+    assert part(_lib.NS_PART_EMIT, row_stats=None) == -5 and "row_stats" in lib.ns_last_error().decode()
+    assert part(_lib.NS_PART_STATS, d=96) == -1 and "hidden size" in lib.ns_last_error().decode()
+    assert part(_lib.NS_PART_EMIT, wsb=16) == -4
+    assert part(_lib.NS_PART_STATS, n=0, hidden=None, teacher=None, labels=None, weights=None, dl=None,
+                row_stats=None, ws=None, wsb=0) == 0
+    assert lib.ns_objective_metrics(p(256), p(256), p(256), 12, 8, 0.1, 0.9, p(256), None) == -1
+    assert lib.ns_objective_metrics(p(256), None, p(256), 8, 8, 0.1, 0.9, p(256), None) == -5
+    assert lib.ns_copy_rows(p(256), 64, 4, p(256), 4, 62, p(512), 64, None) == -1   # row_bytes % 4
+    assert lib.ns_copy_rows(p(256), 32, 4, p(256), 4, 64, p(512), 64, None) == -1   # pitch below the row
+    assert lib.ns_copy_rows(p(256), 64, 4, None, 4, 64, p(512), 64, None) == -5
+    assert lib.ns_copy_rows(p(258), 64, 4, p(256), 4, 64, p(512), 64, None) == -3
+    assert lib.ns_copy_rows(None, 64, 0, None, 0, 64, None, 64, None) == 0            # nothing to copy

@@ -129,6 +129,8 @@ def test_linear_matches_oracle(gpu_lib):
 @pytest.mark.parametrize("n,v,d", [
     (300, 8200, 320),      # ragged token and d tiles, partial last K stage
     (2048, 16384, 2048),   # 8 x 8 tiles x 16 K splits: the XCD-blocked tile order
+    (18432, 2048, 1024),   # 72 x 4 tiles x 4 K splits: 36 XCD blocks, the grid padded to 40 (whole rounds)
+    (18432, 2048, 1000),   # the same with a partial last d tile
 ])
 def test_dh_gemm_alone(gpu_lib, n, v, d):
     g = torch.Generator(device=DEV).manual_seed(3)
