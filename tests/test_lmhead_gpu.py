@@ -167,3 +167,22 @@ def test_kernel_timer_times_only_the_selected_launches(gpu_lib):
         head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov)
         torch.cuda.synchronize()
     assert {"head_stats", "merge_rows", "head_emit", "finalize_metrics"} <= set(kt.times)
+
+
+def test_head_launched_by_round(gpu_lib):
+    """72 token tiles x 32 vocab splits: nine rounds of XCD blocks, each its own launch of the head
+    kernels (past five rounds).  Every row's statistics and the metrics against the oracle, dl and
+    dh on whole blocks."""
+    n, d, v = 18432, 64, 8192
+    hidden, weight, markov, teacher, slots = synthetic.head_inputs(n, d, v, 1801, DEV, ragged=True)
+    o = Objective(block_size=8)
+    m, saved, dh, dl = _run(hidden, weight, markov, teacher, slots, o)
+    z, m_ref, rows, dl_ref, dh_ref = _oracle_head(hidden, weight, markov, teacher, slots, o, dtype=np.float32)
+    _assert_metrics(_metrics(m), m_ref)
+    rs = _np(saved.row_stats)
+    np.testing.assert_allclose(rs[:, 0], rows["lse_z"], rtol=2e-6, atol=5e-5)
+    np.testing.assert_allclose(rs[:, 4], rows["accept_rate"], atol=1e-5)
+    blocks = np.arange(0, n, 977 * 8)   # a block every 977 blocks
+    sel = (blocks[:, None] + np.arange(8)).reshape(-1)
+    _assert_dl(_np(dl).reshape(n, -1)[sel], dl_ref[sel])
+    assert_dh_rows(_np(dh).reshape(n, -1)[sel], dh_ref[sel])
