@@ -117,6 +117,12 @@ class _Compact:
     dl: torch.Tensor       # [m, V] bf16
     index: torch.Tensor    # [N] int64
 
+    def expand(self) -> torch.Tensor:
+        """The [N, V] dl: the kept rows in place, zero rows between (ns_copy_rows)."""
+        n = self.index.shape[0]
+        return _lib.copy_rows(self.dl, self.index, n,
+                              torch.empty((n, self.dl.shape[1]), dtype=self.dl.dtype, device=self.dl.device))
+
 
 @dataclass
 class HeadActivations:
@@ -233,8 +239,10 @@ def _forward_skipping_masked(o, lm_head_weight, hidden_shape, h, ldh, w, ldw, m,
     """lm_head_ce_kl_loss(skip_masked_rows=True): pass 1 on every row, pass 2 on the rows whose
     dl is not all zero -- their hidden and Markov rows gathered into compact copies
     (ns_copy_rows), their teacher rows read in place through the teacher-row gather of the
-    kernels' loads -- their dl scattered back among zero rows, the metrics from every row's
-    statistics.  At C3 (18,326 of 32,768 rows kept) reading the teacher rows in place instead of
+    kernels' loads -- the metrics from every row's statistics.  The compact dl is kept with
+    each row's index among the kept ones; the backward runs the dh GEMM on it and scatters dh
+    among zero rows, and forms the [N, V] dl (zero rows between) only for a caller that asks
+    for it (return_dlogits, final_norm).  At C3 (18,326 of 32,768 rows kept) reading the teacher rows in place instead of
     copying them saved 3.9 of 12.7 ms of copies per step and left pass 2's time unchanged."""
     lib = _lib.load()
     st = _lib.stream(device)
@@ -257,9 +265,9 @@ def _forward_skipping_masked(o, lm_head_weight, hidden_shape, h, ldh, w, ldw, m,
     need = (valid != 0) | (wts != 0) | ~torch.isfinite(row_stats[:, 0]) | ~torch.isfinite(row_stats[:, 1])
     act = torch.nonzero(need).reshape(-1)   # reads the count on the host: it sizes the compacted pass
     rows = act.numel()
-    dl = torch.empty((n, vocab), dtype=torch.bfloat16, device=device)
-    compact = None
+    dl = compact = None
     if rows == n:
+        dl = torch.empty((n, vocab), dtype=torch.bfloat16, device=device)
         part(_lib.NS_PART_EMIT, h, ldh, m, ldm, u, ldu, y, wts, n, dl, row_stats)
     else:
         hc = _lib.copy_rows(h, act, rows, torch.empty((rows, d), dtype=h.dtype, device=device))
@@ -276,8 +284,7 @@ def _forward_skipping_masked(o, lm_head_weight, hidden_shape, h, ldh, w, ldw, m,
         row_stats[:, 4].masked_fill_(~need, 0.0)   # (accept_rate * valid) is 0 there either way
         index = torch.full((n,), -1, dtype=torch.int64, device=device)
         index.index_copy_(0, act, torch.arange(rows, dtype=torch.int64, device=device))
-        _lib.copy_rows(dlc, index, n, dl)
-        compact = _Compact(dlc, index)
+        compact = _Compact(dlc, index)   # the [N, V] dl is formed only if a caller asks for it
     metrics = torch.empty(6, dtype=torch.float32, device=device)
     status = lib.ns_objective_metrics(_lib.ptr(row_stats), _lib.ptr(wts), _lib.ptr(valid), n, k, float(o.ce),
                                       float(o.kl), _lib.ptr(metrics), st)
@@ -444,26 +451,24 @@ def lm_head_ce_kl_backward(saved: HeadActivations, accumulation_steps=1, *, retu
         raise ValueError("accumulation_steps must be >= 1")
     dl, saved.dlogits = saved.dlogits, None   # handed over once, so it is freed after dh unless returned
     compact, saved.compact = saved.compact, None
-    if dl is not None and accumulation_steps != saved.accumulation_steps:
+    if accumulation_steps != saved.accumulation_steps and (dl is not None or compact is not None):
         ratio = _lib.pow2_ratio(saved.accumulation_steps, accumulation_steps)
         if ratio is not None:
-            _lib.scale_inplace(dl, ratio)   # the bits an emission for this count has
-            if compact is not None:
-                _lib.scale_inplace(compact.dl, ratio)
+            # the bits an emission for this count has
+            _lib.scale_inplace(compact.dl if compact is not None else dl, ratio)
         else:
             dl = compact = None
-    if dl is None:
+    if compact is not None:
+        if markov_grads is None and final_norm is None:
+            # dh of the rows pass 2 ran on, scattered among the zero rows of the others
+            dhc = lm_head_linear_backward(compact.dl, saved.weight)
+            n, d = compact.index.shape[0], saved.weight.shape[1]
+            dh = _lib.copy_rows(dhc, compact.index, n, torch.empty((n, d), dtype=torch.bfloat16, device=dhc.device))
+            dh = dh.view(saved.shape[:-1] + (d,))
+            return (dh, compact.expand().view(saved.shape)) if return_dlogits else dh
+        dl = compact.expand()
+    elif dl is None:
         dl = _reemit_dlogits(saved, accumulation_steps)
-    if compact is not None and markov_grads is None and final_norm is None:
-        # dh of the rows pass 2 ran on, scattered among the zero rows of the others
-        dhc = lm_head_linear_backward(compact.dl, saved.weight)
-        d = saved.weight.shape[1]
-        dh = _lib.copy_rows(dhc, compact.index, dl.shape[0],
-                            torch.empty((dl.shape[0], d), dtype=torch.bfloat16, device=dl.device))
-        del dhc, compact
-        dl = dl.view(saved.shape)
-        dh = dh.view(saved.shape[:-1] + (d,))
-        return (dh, dl) if return_dlogits else dh
     del compact
     if markov_grads is not None:
         if saved.markov is None:
