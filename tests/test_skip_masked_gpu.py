@@ -149,3 +149,31 @@ def test_skip_with_every_row_unsupervised(gpu_lib):
         assert torch.equal(getattr(full[0], f), getattr(skip[0], f)), f
     assert not skip[3].any() and not skip[2].any()
     assert torch.equal(full[3], skip[3])
+
+
+def test_skip_with_final_norm_and_dl_formed_on_request(gpu_lib):
+    """The skipping forward keeps the compact dl; a backward that needs the [N, V] dl (the fused
+    final_norm backward, or return_dlogits) forms it from the kept rows: dx, the norm weight's
+    gradient and dl bit for bit those of the full pass, also after a power-of-two rescale."""
+    from nanospec_amd import ops
+
+    n, d, v = 512, 256, 4096
+    hidden0, weight, markov, teacher, slots = synthetic.head_inputs(n, d, v, 5601, DEV, ragged=True)
+    w = torch.ones(d, dtype=torch.bfloat16, device=DEV)
+    hidden, saved_norm = ops.rms_norm(hidden0, w, 1e-6)
+    o = Objective(block_size=8)
+    for bwd_acc in (1, 2):
+        out = []
+        for skip in (False, True):
+            _, saved = head.lm_head_ce_kl_loss(hidden, weight, teacher, slots, o, markov_logits=markov,
+                                               skip_masked_rows=skip)
+            if skip:
+                assert saved.dlogits is None and saved.compact is not None
+            wg = torch.empty(d, dtype=torch.bfloat16, device=DEV)
+            dx, dl = head.lm_head_ce_kl_backward(saved, bwd_acc, return_dlogits=True,
+                                                 final_norm=(saved_norm, w, wg))
+            out.append((dx, dl, wg))
+        torch.cuda.synchronize()
+        (dxf, dlf, wgf), (dxs, dls, wgs) = out
+        assert torch.equal(dlf, dls)
+        assert torch.equal(dxf, dxs) and torch.equal(wgf, wgs)
